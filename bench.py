@@ -1,0 +1,243 @@
+#!/usr/bin/env python3
+"""Headline benchmark: frames/s of the ~1B driving-model analogue at batch 1
+on one MI355X, replayed as one hipGraph per frame, plus per-kernel roofline
+fractions and the CPU oracle timed on the same host.
+
+    python bench.py [--gpus 1] [--steps 50] [--warmup 5] [--spec big_driving_1b]
+                    [--cpu-frames 1] [--no-cpu] [--no-micro]
+
+A step is one frame: inputs (uint8 frame pair + packed f32 vector) already
+resident in HBM, one hipGraph launch of the whole plan (queues, conv stem,
+20 transformer blocks, temporal GEMV, GRU, heads), the frame's hidden state
+fed back on device into the next frame's prev_feat.  K steps are launched
+back to back and bracketed by stream synchronisation.  Prints one JSON line.
+"""
+import argparse
+import json
+import os
+import re
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, 'chestnut-on-pc_amd')):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+PEAK_HBM_GBS = 8000.0          # MI355X HBM3E
+PEAK_F16_TFLOPS = 2500.0       # MI355X dense f16 MFMA
+METRIC = 'frames/sec batch-1 (1B model, 1 GPU) + per-kernel HBM GB/s % of peak'
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def family(name):
+    return re.sub(r'^blk\d+\.', 'blk.', name)
+
+
+def kernel_table(eng, reps=3):
+    """Per plan-family timing: each family's launches run back to back,
+    `reps` times, between HIP events on the engine stream."""
+    plan = eng.plan()
+    fams = {}
+    for i, e in enumerate(plan):
+        fams.setdefault(family(e['name']), []).append(i)
+    rows = []
+    for fam, idx in fams.items():
+        ms = eng.time_launches(idx, reps) / (len(idx) * reps)
+        fl = sum(plan[i]['flops'] for i in idx) / len(idx)
+        by = sum(plan[i]['bytes'] for i in idx) / len(idx)
+        us = ms * 1e3
+        tf = fl / (ms * 1e-3) / 1e12 if fl else 0.0
+        gb = by / (ms * 1e-3) / 1e9
+        kern = plan[idx[0]]['kernel']
+        bound = 'mfma' if (kern.startswith('gemm') or kern == 'attention') and fl / max(by, 1) > 312 else 'hbm'
+        rows.append({'name': fam, 'kernel': kern, 'launches_per_frame': len(idx), 'us_avg': round(us, 2),
+                     'us_per_frame': round(us * len(idx), 2), 'flops': fl, 'bytes': by,
+                     'tflops': round(tf, 2), 'gbs': round(gb, 1), 'bound': bound,
+                     'frac': round(tf / PEAK_F16_TFLOPS if bound == 'mfma' else gb / PEAK_HBM_GBS, 4)})
+    rows.sort(key=lambda r: -r['us_per_frame'])
+    return rows, plan, fams
+
+
+def micro(torch):
+    """BASELINE configs 1 and 2 as single kernels, cold-cache (rotating copies
+    larger than the 256 MB Infinity Cache), HIP events on torch's stream."""
+    from chestnut import kernels as K
+    res = {}
+    n_copies = 5
+    W = [torch.randn(3072, 12288, device='cuda', dtype=torch.float16) * 0.02 for _ in range(n_copies)]
+    x = torch.rand(12288, device='cuda') * 2 - 1
+    y = torch.empty(3072, device='cuda')
+    for w in W:
+        K.gemv(w, x, out=y)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    reps = 20
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(reps):
+        for w in W:
+            K.gemv(w, x, out=y)
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / (reps * n_copies)
+    by = 3072 * 12288 * 2 + 12288 * 4 + 3072 * 4
+    res['gemv_config2'] = {'shape': [3072, 12288], 'us': round(us, 2), 'gbs': round(by / us / 1e3, 1),
+                           'frac_hbm': round(by / us / 1e3 / PEAK_HBM_GBS, 4), 'copies': n_copies}
+    del W
+    n_copies = 12
+    A = [torch.randn(1024, 6144, device='cuda', dtype=torch.float16) / 78.4 for _ in range(n_copies)]
+    B = [torch.randn(6144, 1024, device='cuda', dtype=torch.float16) / 78.4 for _ in range(n_copies)]
+    C = torch.empty(1024, 1024, device='cuda')
+    tile, split, nb = K.gemm_workspace(1024, 1024, 6144, True)
+    ws = torch.empty(max(nb // 4, 1), device='cuda')
+    for a, b in zip(A, B):
+        K.gemm(a, b, out=C, workspace=ws)
+    reps = 10
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(reps):
+        for a, b in zip(A, B):
+            K.gemm(a, b, out=C, workspace=ws)
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / (reps * n_copies)
+    fl = 2.0 * 1024 * 1024 * 6144
+    res['gemm_config1'] = {'shape': [1024, 6144, 1024], 'us': round(us, 2), 'tflops': round(fl / us / 1e6, 1),
+                           'frac_mfma': round(fl / us / 1e6 / PEAK_F16_TFLOPS, 4), 'tile': tile, 'split_k': split,
+                           'copies': n_copies}
+    return res
+
+
+def cpu_baseline(sp, weights, n_frames, warped, packed):
+    """The numpy oracle (f32 OpenBLAS) on this host's cores, bounded sample."""
+    from threadpoolctl import threadpool_limits
+    from oracle.model import OracleModel
+    cores = min(16, len(os.sched_getaffinity(0)))
+    with threadpool_limits(limits=cores):
+        orc = OracleModel(sp, weights, acc=np.float32)
+        t0 = time.perf_counter()
+        pk = packed.copy()
+        for _ in range(n_frames):
+            o = orc.run_frame(warped, pk)
+            pk[12:] = o[-sp['hidden']:]
+        dt = time.perf_counter() - t0
+    cpu = ''
+    try:
+        with open('/proc/cpuinfo') as fh:
+            cpu = next((l.split(':', 1)[1].strip() for l in fh if l.startswith('model name')), '')
+    except OSError:
+        pass
+    return {'value': round(n_frames / dt, 4), 'unit': 'frames/s', 'cores': cores, 'kind': 'port',
+            'sample': f'{n_frames} frame(s) of {sp["name"]} through oracle/model.py (numpy f32, OpenBLAS), '
+                      f'{dt:.1f} s; host CPU: {cpu}'}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument('--gpus', type=int, default=1)
+    ap.add_argument('--steps', type=int, default=50)
+    ap.add_argument('--warmup', type=int, default=5)
+    ap.add_argument('--spec', default='big_driving_1b')
+    ap.add_argument('--cpu-frames', type=int, default=1)
+    ap.add_argument('--no-cpu', action='store_true')
+    ap.add_argument('--no-micro', action='store_true')
+    a = ap.parse_args()
+    if a.gpus != 1 or int(os.environ.get('WORLD_SIZE', '1')) != 1:
+        sys.exit('bench.py measures one GPU only: this build has no multi-GPU path '
+                 '(a recurrent batch-1 frame does not shard; see DESIGN.md). Run with --gpus 1.')
+
+    import torch
+    assert torch.cuda.is_available(), 'bench.py needs a GPU'
+    from chestnut import Engine, spec as S
+
+    sp = S.get_spec(a.spec)
+    t0 = time.perf_counter()
+    weights = S.make_weights(sp)
+    log(f'[bench] {sp["name"]}: {S.param_count(sp) / 1e6:.1f}M params generated in {time.perf_counter() - t0:.1f}s')
+    eng = Engine(sp, weights=weights)
+    rng = np.random.default_rng(42)
+    warped = rng.integers(0, 256, (2, 6, sp['img_h'], sp['img_w']), dtype=np.uint8)
+    packed = np.zeros(sp['desire_len'] + 4 + sp['feat_len'], np.float32)
+    packed[8:10] = (1.0, 0.0)
+
+    # host API frames (graph capture on the first), then the PCIe-inclusive rate
+    t0 = time.perf_counter()
+    out = eng.run_frame(warped, packed)
+    log(f'[bench] first frame (capture + run) {time.perf_counter() - t0:.3f}s, graph nodes {eng.graph_nodes()}, '
+        f'finite={bool(np.all(np.isfinite(out)))}')
+    pk = packed.copy()
+    n_host = 20
+    t0 = time.perf_counter()
+    for _ in range(n_host):
+        o = eng.run_frame(warped, pk)
+        pk[12:] = o[eng.out_slices['hidden_state']]
+    host_fps = n_host / (time.perf_counter() - t0)
+
+    # device-resident frames: inputs in HBM, back-to-back graph launches
+    eng.write('warped', warped)
+    eng.write('packed', packed)
+    for _ in range(a.warmup):
+        eng.frame_launch()
+    eng.synchronize()
+    s = torch.cuda.ExternalStream(eng.stream())
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    eng.synchronize()
+    t0 = time.perf_counter()
+    e0.record(s)
+    for _ in range(a.steps):
+        eng.frame_launch()
+    e1.record(s)
+    eng.synchronize()
+    wall = time.perf_counter() - t0
+    torch.cuda.synchronize()
+    gpu_ms = e0.elapsed_time(e1)
+    fps = a.steps / wall
+    log(f'[bench] {a.steps} frames: wall {wall * 1e3:.2f} ms ({fps:.1f} fps), events {gpu_ms:.2f} ms, '
+        f'host-inclusive {host_fps:.1f} fps')
+
+    rows, plan, fams = kernel_table(eng)
+    for r in rows[:12]:
+        log(f'[bench]   {r["name"]:16s} {r["kernel"]:22s} x{r["launches_per_frame"]:3d} {r["us_avg"]:9.2f} us '
+            f'{r["tflops"]:8.1f} TF/s {r["gbs"]:8.1f} GB/s frac {r["frac"]:.3f} ({r["bound"]})')
+    dom = rows[0]
+    idx = fams[dom['name']]
+    reps = max(1, int(200 / len(idx)))
+    ms = eng.time_launches(idx, reps) / (len(idx) * reps)
+    if dom['bound'] == 'mfma':
+        ach, peak, unit = dom['flops'] / (ms * 1e-3) / 1e12, PEAK_F16_TFLOPS, 'TFLOP/s'
+    else:
+        ach, peak, unit = dom['bytes'] / (ms * 1e-3) / 1e9, PEAK_HBM_GBS, 'GB/s'
+    roof = {'kernel': dom['name'] + ' (' + dom['kernel'] + ')', 'bound': dom['bound'], 'achieved': round(ach, 2),
+            'peak': peak, 'unit': unit, 'frac': round(ach / peak, 4), 'traffic': None,
+            'us_per_launch': round(ms * 1e3, 2), 'launches_timed': len(idx) * reps,
+            'algorithmic_per_launch': dom['flops'] if dom['bound'] == 'mfma' else dom['bytes']}
+
+    line = {'metric': METRIC, 'value': round(fps, 2), 'unit': 'frames/s', 'n_gpus': 1, 'steps': a.steps,
+            'warmup': a.warmup, 'ms_per_step': round(wall * 1e3 / a.steps, 4), 'higher_is_better': True,
+            'scaling': 'weak', 'vs_baseline': None, 'dtype': 'f16',
+            'data': 'synthetic (seeded uniform uint8 frames, seeded N(0,0.02) f16 weights)',
+            'config': {'workload': f'{sp["name"]}: BASELINE config 5, batch-1 frame (conv stem -> '
+                                   f'{sp["n_layers"]} blocks d={sp["d_model"]} {sp["n_heads"]}x{sp["head_dim"]} '
+                                   f'MLP {sp["d_ff"]}, {sp["stem"][-1]} tokens -> temporal GEMV, GRU, heads)',
+                       'params': S.param_count(sp), 'graph_nodes': eng.graph_nodes(), 'launches': len(plan),
+                       'event_ms_per_step': round(gpu_ms / a.steps, 4),
+                       'host_inclusive_fps': round(host_fps, 2)},
+            'roofline': roof, 'kernels': rows}
+    if not a.no_micro:
+        line['micro'] = micro(torch)
+        log(f'[bench] micro {line["micro"]}')
+    eng.close()
+    if not a.no_cpu:
+        line['cpu_baseline'] = cpu_baseline(sp, weights, a.cpu_frames, warped, packed)
+        log(f'[bench] cpu baseline {line["cpu_baseline"]}')
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == '__main__':
+    main()

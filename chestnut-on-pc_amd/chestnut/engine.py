@@ -1,0 +1,215 @@
+"""Python surface of the frame engine, mirroring the reference's namespace.
+
+The reference's callers `exec` run_pinned2.py up to '# --- smoke run' and use
+`run_frame(warped_np, packed)`, `out_slices`, `img`, `make_warped`, `PACKED`
+(run_pinned2.py:1353-1389, 1462-1565; video_check.py:18-19, 59-60).
+`Engine` provides the same names over the native library; `load(spec)`
+returns a namespace with exactly those attributes.
+"""
+import ctypes
+import json
+import types
+from concurrent.futures import ThreadPoolExecutor
+
+import numpy as np
+
+from . import spec as _spec
+from ._lib import call, lib
+
+_DT = {0: np.float32, 1: np.float16, 2: np.uint8, 3: np.uint32}
+
+
+class Engine:
+    """One model on one GPU: parameters, queues, plan and hipGraph.
+
+    spec: spec name ('driving_39m', 'big_driving_1b', 'tiny') or dict.
+    weights: dict name -> array; None generates the seeded weights.
+    """
+
+    def __init__(self, spec='big_driving_1b', weights=None, seed=None, graph=True, gen_threads=8):
+        self.spec = _spec.get_spec(spec)
+        if seed is not None:
+            self.spec['seed'] = int(seed)
+        h = ctypes.c_void_p()
+        call('ck_create', _spec.spec_json(self.spec).encode(), ctypes.byref(h))
+        self._h = h
+        try:
+            self._check_param_table()
+            self.upload_weights(weights, gen_threads)
+            n = ctypes.c_int()
+            call('ck_output_size', self._h, ctypes.byref(n))
+            self.n_out = n.value
+            buf = ctypes.create_string_buffer(1 << 14)
+            call('ck_output_slices', self._h, buf, len(buf))
+            self.out_slices = {k: slice(v[0], v[1]) for k, v in json.loads(buf.value.decode()).items()}
+            self.set_graph(graph)
+        except Exception:
+            self.close()
+            raise
+        s = self.spec
+        self.img = (1, 6 * s['n_frames'], s['img_h'], s['img_w'])
+        self.PACKED = np.zeros(s['desire_len'] + 4 + s['feat_len'], np.float32)
+
+    # -- lifecycle --------------------------------------------------------------
+    def close(self):
+        if getattr(self, '_h', None):
+            lib().ck_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    # -- parameters -------------------------------------------------------------
+    def param_names(self):
+        n = ctypes.c_int()
+        call('ck_param_count', self._h, ctypes.byref(n))
+        out = []
+        name = ctypes.create_string_buffer(256)
+        nb = ctypes.c_size_t()
+        dt = ctypes.c_int()
+        for i in range(n.value):
+            call('ck_param_info', self._h, i, name, len(name), ctypes.byref(nb), ctypes.byref(dt))
+            out.append((name.value.decode(), nb.value, _DT[dt.value]))
+        return out
+
+    def _check_param_table(self):
+        native = self.param_names()
+        table = _spec.param_table(self.spec)
+        if [n for n, _, _ in native] != [t[0] for t in table]:
+            raise RuntimeError('native and Python parameter tables disagree')
+        for (n, nb, dt), (_, shape, tdt, _, _) in zip(native, table):
+            want = int(np.prod(shape)) * (2 if tdt == 'f16' else 4)
+            if nb != want:
+                raise RuntimeError(f'parameter {n}: native {nb} bytes, table {want}')
+
+    def upload_weights(self, weights=None, threads=8):
+        """Upload `weights` (or the spec's seeded weights, generated on the fly)."""
+        table = _spec.param_table(self.spec)
+        seed = self.spec['seed']
+
+        def one(p):
+            name = p[0]
+            arr = weights[name] if weights is not None else _spec.make_param(seed, *p)
+            arr = np.ascontiguousarray(arr, dtype=np.float16 if p[2] == 'f16' else np.float32)
+            call('ck_upload_param', self._h, name.encode(), arr.ctypes.data, arr.nbytes)
+
+        with ThreadPoolExecutor(max_workers=max(1, threads)) as ex:
+            list(ex.map(one, table))
+
+    # -- frames -----------------------------------------------------------------
+    def run_frame(self, warped_np, packed):
+        """One policy frame (run_pinned2.py:1462-1565): uint8 [2,6,H,W] and
+        f32 [524] in, flat f32 output vector out."""
+        w = np.ascontiguousarray(warped_np, dtype=np.uint8)
+        p = np.ascontiguousarray(packed, dtype=np.float32)
+        s = self.spec
+        if w.shape != (2, 6, s['img_h'], s['img_w']):
+            raise ValueError(f'warped must be uint8 {(2, 6, s["img_h"], s["img_w"])}, got {w.shape}')
+        if p.shape != self.PACKED.shape:
+            raise ValueError(f'packed must be f32 {self.PACKED.shape}, got {p.shape}')
+        out = np.empty(self.n_out, np.float32)
+        call('ck_run_frame', self._h, w.ctypes.data, p.ctypes.data, out.ctypes.data)
+        return out
+
+    def make_warped(self, val=128):
+        """Constant frame pair (run_pinned2.py:1388-1389)."""
+        s = self.spec
+        return np.full((2, 6, s['img_h'], s['img_w']), val, np.uint8)
+
+    def set_graph(self, on):
+        call('ck_set_graph', self._h, 1 if on else 0)
+
+    def graph_nodes(self):
+        n = ctypes.c_size_t()
+        call('ck_graph_nodes', self._h, ctypes.byref(n))
+        return n.value
+
+    def reset(self):
+        call('ck_reset', self._h)
+
+    def frame_launch(self):
+        call('ck_frame_launch', self._h)
+
+    def synchronize(self):
+        call('ck_synchronize', self._h)
+
+    def stream(self):
+        s = ctypes.c_void_p()
+        call('ck_stream', self._h, ctypes.byref(s))
+        return s.value
+
+    # -- plan / profiling ------------------------------------------------------
+    def plan(self):
+        n = ctypes.c_int()
+        call('ck_plan_size', self._h, ctypes.byref(n))
+        name = ctypes.create_string_buffer(128)
+        kern = ctypes.create_string_buffer(128)
+        fl, by = ctypes.c_double(), ctypes.c_double()
+        out = []
+        for i in range(n.value):
+            call('ck_plan_entry', self._h, i, name, len(name), kern, len(kern), ctypes.byref(fl), ctypes.byref(by))
+            out.append({'name': name.value.decode(), 'kernel': kern.value.decode(), 'flops': fl.value,
+                        'bytes': by.value})
+        return out
+
+    def plan_index(self, name):
+        for i, e in enumerate(self.plan()):
+            if e['name'] == name:
+                return i
+        raise KeyError(name)
+
+    def kernel_times(self):
+        """One eager frame with per-launch event timing (KSYNC)."""
+        plan = self.plan()
+        ms = (ctypes.c_float * len(plan))()
+        call('ck_kernel_times', self._h, ms, len(plan))
+        for e, t in zip(plan, ms):
+            e['ms'] = float(t)
+        return plan
+
+    def run_range(self, first, last):
+        call('ck_run_range', self._h, int(first), int(last))
+
+    def time_launches(self, indices, reps=1):
+        """Elapsed ms of launching plan entries `indices` in order, `reps`
+        times, between HIP events on the engine stream."""
+        idx = (ctypes.c_int * len(indices))(*indices)
+        ms = ctypes.c_float()
+        call('ck_time_launches', self._h, idx, len(indices), int(reps), ctypes.byref(ms))
+        return ms.value
+
+    # -- tensors ----------------------------------------------------------------
+    def tensor_ptr(self, name):
+        p = ctypes.c_void_p()
+        nb = ctypes.c_size_t()
+        call('ck_tensor', self._h, name.encode(), ctypes.byref(p), ctypes.byref(nb))
+        return p.value, nb.value
+
+    def read(self, name, dtype, shape=None):
+        _, nb = self.tensor_ptr(name)
+        dtype = np.dtype(dtype)
+        count = nb // dtype.itemsize if shape is None else int(np.prod(shape))
+        out = np.empty(count, dtype)
+        call('ck_read_tensor', self._h, name.encode(), out.ctypes.data, out.nbytes)
+        return out if shape is None else out.reshape(shape)
+
+    def write(self, name, arr):
+        arr = np.ascontiguousarray(arr)
+        call('ck_write_tensor', self._h, name.encode(), arr.ctypes.data, arr.nbytes)
+
+
+def load(spec='big_driving_1b', **kw):
+    """The reference's exec-prefix namespace (run_pinned2.py:1346-1572):
+    run_frame, out_slices, img, make_warped, PACKED, plus the engine."""
+    eng = Engine(spec, **kw)
+    return types.SimpleNamespace(run_frame=eng.run_frame, out_slices=eng.out_slices, img=eng.img,
+                                 make_warped=eng.make_warped, PACKED=eng.PACKED, engine=eng)

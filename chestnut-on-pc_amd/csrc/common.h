@@ -1,0 +1,118 @@
+// Shared definitions for the chestnut gfx950 library: error convention,
+// vector types, wave-level reductions and the image2d texel addressing rule.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <stdexcept>
+#include <string>
+
+namespace ck {
+
+struct Error : std::runtime_error {
+  using std::runtime_error::runtime_error;
+};
+
+void set_last_error(const std::string& msg);
+
+#define CK_HIP(call)                                                                 \
+  do {                                                                               \
+    hipError_t e_ = (call);                                                          \
+    if (e_ != hipSuccess)                                                            \
+      throw ::ck::Error(std::string(#call) + " failed: " + hipGetErrorString(e_));   \
+  } while (0)
+
+#define CK_REQUIRE(cond, msg)                                                        \
+  do {                                                                               \
+    if (!(cond)) throw ::ck::Error(std::string(msg));                                \
+  } while (0)
+
+// Launch check: a launch error (bad grid, invalid symbol) surfaces here.
+#define CK_LAUNCHED(what) CK_HIP(hipGetLastError())
+
+typedef _Float16 half_t;
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+typedef float float16_t __attribute__((ext_vector_type(16)));
+
+// ---------------------------------------------------------------------------
+// Wave64 reductions.  Lanes 0..63 of a CDNA wave form 4 DPP rows of 16.
+// Inside a row: xor-1 and xor-2 exchanges (quad_perm), then the half-row and
+// row mirrors; every lane then holds its row's sum, bit-identical across the
+// row (each step adds the same two operands, only commuted).  The four row
+// sums are combined with readlane in a fixed order, so the result is
+// deterministic and identical in every lane.
+// ---------------------------------------------------------------------------
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+constexpr int DPP_QUAD_1032 = 0xB1;   // quad_perm [1,0,3,2]  (xor 1)
+constexpr int DPP_QUAD_2301 = 0x4E;   // quad_perm [2,3,0,1]  (xor 2)
+constexpr int DPP_ROW_HALF_MIRROR = 0x141;
+constexpr int DPP_ROW_MIRROR = 0x140;
+
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp_mov<DPP_QUAD_1032>(v);
+  v += dpp_mov<DPP_QUAD_2301>(v);
+  v += dpp_mov<DPP_ROW_HALF_MIRROR>(v);
+  v += dpp_mov<DPP_ROW_MIRROR>(v);
+  return v;
+}
+
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, dpp_mov<DPP_QUAD_1032>(v));
+  v = fmaxf(v, dpp_mov<DPP_QUAD_2301>(v));
+  v = fmaxf(v, dpp_mov<DPP_ROW_HALF_MIRROR>(v));
+  v = fmaxf(v, dpp_mov<DPP_ROW_MIRROR>(v));
+  return v;
+}
+
+__device__ __forceinline__ float readlane_f32(float v, int lane) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+  v = row16_sum(v);
+  float r0 = readlane_f32(v, 0), r1 = readlane_f32(v, 16);
+  float r2 = readlane_f32(v, 32), r3 = readlane_f32(v, 48);
+  return (r0 + r1) + (r2 + r3);
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+  v = row16_max(v);
+  float r0 = readlane_f32(v, 0), r1 = readlane_f32(v, 16);
+  float r2 = readlane_f32(v, 32), r3 = readlane_f32(v, 48);
+  return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+}
+
+// ---------------------------------------------------------------------------
+// image2d texel read with a zero border (OpenCL CLK_ADDRESS_CLAMP).
+// An image param has A rows of B texels; (y, x) is a texel coordinate.
+//   fl = y*B + x, fc = clamp(fl, 0, A*B-1), valid = 0<=x<B && 0<=y<A,
+//   value = valid ? texel[fc] : 0.
+// The load is always issued at an in-bounds address and masked afterwards.
+// Reference: run_pinned2.py:56-84 (address + predicate), 355-374 (masked load).
+// ---------------------------------------------------------------------------
+template <typename TexelT>
+__device__ __forceinline__ TexelT img_texel_zb(const TexelT* __restrict__ img, int A, int B, int y, int x) {
+  int fl = y * B + x;
+  int fc = min(max(fl, 0), A * B - 1);
+  bool valid = (x >= 0) & (x < B) & (y >= 0) & (y < A);
+  TexelT v = img[fc];
+  return valid ? v : TexelT{};
+}
+
+__device__ __forceinline__ float gelu_tanh(float x) {
+  const float c = 0.7978845608028654f;   // sqrt(2/pi)
+  return 0.5f * x * (1.0f + tanhf(c * (x + 0.044715f * x * x * x)));
+}
+
+__device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+inline int ceil_div(long a, long b) { return (int)((a + b - 1) / b); }
+
+}  // namespace ck

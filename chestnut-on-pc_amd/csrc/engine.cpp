@@ -1,0 +1,543 @@
+// Frame engine: spec -> parameter/activation tensors -> resolved launch plan
+// -> hipGraph, one graph launch per frame.
+//
+// Reference structure being replaced (run_pinned2.py):
+//   1346-1370  model load + graph flatten      -> build_params / build_plan
+//   1372-1389  input queues and PACKED         -> ring buffers + staging tensors
+//   1404-1420  first-frame plan recorder       -> the plan is resolved at create
+//   1432-1502  capture on a stream, instantiate -> capture()
+//   1503-1565  per-frame H2D, cuGraphLaunch, sync, D2H -> run_frame()
+//   1513-1557  KSYNC per-launch event timing    -> kernel_times()
+// Every launch of the plan has static device addresses, so the captured
+// graph replays unchanged; the per-frame state that must move (queue
+// positions, the recurrent hidden state) lives in device memory and is
+// advanced by the plan's own kernels.
+#include "engine.h"
+
+#include <cstring>
+#include <sstream>
+
+#include "json.h"
+
+namespace ck {
+
+namespace {
+
+long round_up(long v, long m) { return (v + m - 1) / m * m; }
+
+int jint(const JVal& o, const char* k, int dflt, bool required = false) {
+  const JVal* v = o.get(k);
+  if (!v) {
+    CK_REQUIRE(!required, std::string("spec: missing key ") + k);
+    return dflt;
+  }
+  CK_REQUIRE(v->kind == JVal::NUM, std::string("spec: key ") + k + " must be a number");
+  return (int)v->num;
+}
+
+}  // namespace
+
+Spec parse_spec(const std::string& json) {
+  JParser jp(json);
+  JVal o = jp.parse();
+  CK_REQUIRE(o.kind == JVal::OBJ, "spec: top level must be an object");
+  Spec s;
+  if (const JVal* v = o.get("name")) s.name = v->str;
+  s.img_h = jint(o, "img_h", 128);
+  s.img_w = jint(o, "img_w", 256);
+  s.n_frames = jint(o, "n_frames", 2);
+  s.fs = jint(o, "frame_skip", 4);
+  s.feat_len = jint(o, "feat_len", 512);
+  s.feat_hist = jint(o, "feat_hist", 24);
+  s.desire_len = jint(o, "desire_len", 8);
+  s.desire_hist = jint(o, "desire_hist", 25);
+  s.hidden = jint(o, "hidden", 512);
+  s.d = jint(o, "d_model", 0, true);
+  s.n_heads = jint(o, "n_heads", 0, true);
+  s.head_dim = jint(o, "head_dim", 0, true);
+  s.n_layers = jint(o, "n_layers", 0, true);
+  s.d_ff = jint(o, "d_ff", 0, true);
+  s.temporal_dim = jint(o, "temporal_dim", 0, true);
+  if (const JVal* v = o.get("ln_eps")) s.eps = (float)v->num;
+  const JVal* st = o.get("stem");
+  CK_REQUIRE(st && st->kind == JVal::ARR && !st->arr.empty(), "spec: stem must be a non-empty array");
+  for (const auto& e : st->arr) s.stem.push_back((int)e.num);
+  if (const JVal* ou = o.get("outputs")) {
+    CK_REQUIRE(ou->kind == JVal::ARR, "spec: outputs must be an array of [name, size]");
+    for (const auto& e : ou->arr) {
+      CK_REQUIRE(e.kind == JVal::ARR && e.arr.size() == 2, "spec: outputs entries are [name, size]");
+      s.outputs.emplace_back(e.arr[0].str, (int)e.arr[1].num);
+    }
+  }
+  // structural requirements of the kernels
+  CK_REQUIRE(s.n_frames == 2, "spec: n_frames must be 2 (two sampled frames per stream)");
+  CK_REQUIRE(s.d == s.n_heads * s.head_dim, "spec: d_model must equal n_heads * head_dim");
+  CK_REQUIRE(s.hidden == s.feat_len, "spec: hidden must equal feat_len (prev_feat is the GRU state)");
+  CK_REQUIRE(s.img_h % (1 << s.stem.size()) == 0 && s.img_w % (1 << s.stem.size()) == 0,
+             "spec: image size must divide by 2^len(stem)");
+  for (int c : s.stem) CK_REQUIRE(c % 8 == 0, "spec: stem channels must be multiples of 8");
+  CK_REQUIRE(s.temporal_dim % 8 == 0 && s.d % 64 == 0 && s.d_ff % 64 == 0, "spec: widths must be multiples of 64");
+  return s;
+}
+
+}  // namespace ck
+
+using namespace ck;
+
+ck_engine::ck_engine(const std::string& spec_json) : sp(parse_spec(spec_json)) {
+  T = sp.stem.back();
+  n_spatial = (sp.img_h >> sp.stem.size()) * (sp.img_w >> sp.stem.size());
+  n_head_out = 0;
+  for (auto& o : sp.outputs) n_head_out += o.second;
+  n_out = n_head_out + sp.hidden;
+  n_ctx = sp.temporal_dim + sp.desire_hist * sp.desire_len + 4;
+  ld_ctx = (int)round_up(n_ctx, 8);
+  packed_len = sp.desire_len + 4 + sp.feat_len;
+  warped_bytes = 2ull * 6 * sp.img_h * sp.img_w;
+  CK_REQUIRE(T % 64 == 0 && T <= 512, "spec: token count (last stem width) must be a multiple of 64, <= 512");
+  CK_REQUIRE(2 * n_spatial % 64 == 0, "spec: token features must be a multiple of 64");
+  CK_HIP(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking));
+  build_params();
+  build_activations();
+  build_plan();
+  CK_HIP(hipHostMalloc((void**)&h_warped, warped_bytes, hipHostMallocDefault));
+  CK_HIP(hipHostMalloc((void**)&h_packed, packed_len * sizeof(float), hipHostMallocDefault));
+  CK_HIP(hipHostMalloc((void**)&h_out, n_out * sizeof(float), hipHostMallocDefault));
+  reset_state();
+}
+
+ck_engine::~ck_engine() {
+  if (stream) (void)hipStreamSynchronize(stream);
+  drop_graph();
+  for (auto& t : tensors)
+    if (t.ptr) (void)hipFree(t.ptr);
+  if (ws) (void)hipFree(ws);
+  if (h_warped) (void)hipHostFree(h_warped);
+  if (h_packed) (void)hipHostFree(h_packed);
+  if (h_out) (void)hipHostFree(h_out);
+  if (stream) (void)hipStreamDestroy(stream);
+}
+
+Tensor& ck_engine::add_tensor(const std::string& name, size_t nbytes, int dtype, bool param, long rows, long cols,
+                              long ld) {
+  CK_REQUIRE(by_name.count(name) == 0, "duplicate tensor " + name);
+  Tensor t;
+  t.name = name;
+  t.nbytes = nbytes;
+  t.dtype = dtype;
+  t.param = param;
+  const size_t esz = dtype == DT_F16 ? 2 : dtype == DT_U8 ? 1 : 4;
+  if (cols == 0) { rows = 1; cols = (long)(nbytes / esz); }
+  if (ld == 0) ld = cols;
+  t.rows = rows; t.cols = cols; t.ld = ld;
+  const size_t alloc = std::max<size_t>(256, round_up((long)(rows * ld * esz), 256));
+  CK_HIP(hipMalloc(&t.ptr, alloc));
+  CK_HIP(hipMemset(t.ptr, 0, alloc));
+  by_name[name] = tensors.size();
+  tensors.push_back(t);
+  return tensors.back();
+}
+
+Tensor& ck_engine::tensor(const std::string& name) {
+  auto it = by_name.find(name);
+  CK_REQUIRE(it != by_name.end(), "unknown tensor " + name);
+  return tensors[it->second];
+}
+
+// Parameter table; must list the same names, shapes and dtypes as the
+// Python side (chestnut/spec.py param_table).
+void ck_engine::build_params() {
+  const int d = sp.d, F = sp.d_ff, Hh = sp.hidden;
+  auto f16 = [&](const std::string& n, long numel) { add_tensor(n, numel * 2, DT_F16, true); };
+  auto f32 = [&](const std::string& n, long numel) { add_tensor(n, numel * 4, DT_F32, true); };
+  int ci = 6 * sp.n_frames;
+  for (size_t i = 0; i < sp.stem.size(); ++i) {
+    const int co = sp.stem[i];
+    const long K = 9L * ci;
+    add_tensor("stem." + std::to_string(i) + ".w", 2L * co * K * 2, DT_F16, true, 2L * co, K, round_up(K, 64));
+    f32("stem." + std::to_string(i) + ".b", 2L * co);
+    ci = co;
+  }
+  f16("emb.w", (long)d * 2 * n_spatial);
+  f32("emb.b", d);
+  f16("pos", (long)T * d);
+  f16("tmp.w", (long)sp.temporal_dim * sp.feat_hist * sp.feat_len);
+  f32("tmp.b", sp.temporal_dim);
+  add_tensor("ctx.w", (long)d * n_ctx * 2, DT_F16, true, d, n_ctx, ld_ctx);
+  f32("ctx.b", d);
+  for (int l = 0; l < sp.n_layers; ++l) {
+    const std::string p = "blk." + std::to_string(l) + ".";
+    f32(p + "ln1.g", d); f32(p + "ln1.b", d);
+    f16(p + "qkv.w", 3L * d * d); f32(p + "qkv.b", 3L * d);
+    f16(p + "o.w", (long)d * d); f32(p + "o.b", d);
+    f32(p + "ln2.g", d); f32(p + "ln2.b", d);
+    f16(p + "up.w", (long)F * d); f32(p + "up.b", F);
+    f16(p + "down.w", (long)d * F); f32(p + "down.b", d);
+  }
+  f32("lnf.g", d); f32("lnf.b", d);
+  f16("gru.wih", 3L * Hh * d); f32("gru.bih", 3L * Hh);
+  f16("gru.whh", 3L * Hh * Hh); f32("gru.bhh", 3L * Hh);
+  f16("head.w", (long)n_head_out * Hh); f32("head.b", n_head_out);
+}
+
+void ck_engine::build_activations() {
+  const long HW = (long)sp.img_h * sp.img_w;
+  const int d = sp.d;
+  const int slots = sp.fs * (sp.n_frames - 1) + 1;
+  add_tensor("warped", warped_bytes, DT_U8, false);
+  add_tensor("packed", packed_len * 4, DT_F32, false);
+  add_tensor("out", n_out * 4, DT_F32, false);
+  add_tensor("counter", 4, DT_U32, false);
+  add_tensor("img_ring", 2L * slots * 6 * HW, DT_U8, false);
+  add_tensor("feat_ring", (long)sp.fs * sp.feat_hist * sp.feat_len * 4, DT_F32, false);
+  add_tensor("desire_ring", (long)sp.fs * sp.desire_hist * sp.desire_len * 4, DT_F32, false);
+  add_tensor("img", 2L * 6 * sp.n_frames * HW, DT_U8, false);
+  add_tensor("feat_buf", (long)sp.feat_hist * sp.feat_len * 4, DT_F32, false);
+  add_tensor("ctx_in", (long)ld_ctx * 4, DT_F32, false);
+  long patches = 0;
+  int H = sp.img_h, W = sp.img_w, C = 6 * sp.n_frames;
+  for (size_t i = 0; i < sp.stem.size(); ++i) {
+    const int Ho = (H - 1) / 2 + 1, Wo = (W - 1) / 2 + 1;
+    patches = std::max(patches, 2L * Ho * Wo * round_up(9L * C, 64));
+    add_tensor("stem." + std::to_string(i) + ".out", 2L * Ho * Wo * sp.stem[i] * 2, DT_F16, false);
+    H = Ho; W = Wo; C = sp.stem[i];
+  }
+  add_tensor("patches", patches * 2, DT_F16, false);
+  add_tensor("tokens", (long)T * 2 * n_spatial * 2, DT_F16, false);
+  add_tensor("ctx", (long)d * 4, DT_F32, false);
+  add_tensor("x", (long)T * d * 4, DT_F32, false);
+  add_tensor("h16", (long)T * d * 2, DT_F16, false);
+  add_tensor("qk", (long)T * 2 * d * 2, DT_F16, false);
+  add_tensor("vt", (long)d * T * 2, DT_F16, false);
+  add_tensor("att", (long)T * d * 2, DT_F16, false);
+  add_tensor("u", (long)T * sp.d_ff * 2, DT_F16, false);
+  add_tensor("xf", (long)T * d * 4, DT_F32, false);
+  add_tensor("pooled", (long)d * 4, DT_F32, false);
+  add_tensor("gi", 3L * sp.hidden * 4, DT_F32, false);
+  add_tensor("gh", 3L * sp.hidden * 4, DT_F32, false);
+  add_tensor("h_new", (long)sp.hidden * 4, DT_F32, false);
+}
+
+void ck_engine::add(const std::string& name, const std::string& kernel, double flops, double bytes,
+                    std::function<void(hipStream_t)> fn) {
+  Launch l;
+  l.name = name;
+  l.kernel = kernel;
+  l.flops = flops;
+  l.bytes = bytes;
+  l.fn = std::move(fn);
+  plan.push_back(std::move(l));
+}
+
+void ck_engine::add_gemm(const std::string& name, const std::string& kernel, GemmDesc g) {
+  const size_t need = gemm_plan(g);
+  ws_floats = std::max(ws_floats, need);
+  const double M = g.M, N = g.N, K = g.K, B = g.batch;
+  const bool out32 = g.epi == EPI_F32 || g.epi == EPI_F32_RESID;
+  double bytes = B * (M * K + N * K) * 2 + B * M * N * (out32 ? 4 : 2) + (g.bias ? B * N * 4 : 0);
+  if (g.epi == EPI_F32_RESID) bytes += B * M * N * 4;
+  std::string kern = kernel + (g.split > 1 ? "+splitk" + std::to_string(g.split) : "");
+  ck_engine* self = this;
+  add(name, kern, 2.0 * M * N * K * B, bytes, [self, g](hipStream_t s) {
+    GemmDesc d = g;
+    d.ws = self->ws;
+    d.ws_floats = self->ws_floats;
+    launch_gemm(d, s);
+  });
+}
+
+void ck_engine::build_plan() {
+  plan.clear();
+  const int d = sp.d, F = sp.d_ff, Hh = sp.hidden, dl = sp.desire_len;
+  const long HW = (long)sp.img_h * sp.img_w;
+  auto h16 = [&](const std::string& n) { return static_cast<half_t*>(ptr(n)); };
+  auto f32 = [&](const std::string& n) { return static_cast<float*>(ptr(n)); };
+
+  // 1. policy inputs: queue push + sample (compile_modeld.py:198-212)
+  {
+    QueueDims q{sp.img_h, sp.img_w, sp.fs, sp.fs * (sp.n_frames - 1) + 1, sp.feat_len, sp.feat_hist, sp.desire_len,
+                sp.desire_hist};
+    const uint8_t* warped = static_cast<uint8_t*>(ptr("warped"));
+    const float* packed = f32("packed");
+    const unsigned* counter = static_cast<unsigned*>(ptr("counter"));
+    uint8_t* ring = static_cast<uint8_t*>(ptr("img_ring"));
+    float* fr = f32("feat_ring");
+    float* dr = f32("desire_ring");
+    uint8_t* img = static_cast<uint8_t*>(ptr("img"));
+    float* fb = f32("feat_buf");
+    float* tail = f32("ctx_in") + sp.temporal_dim;
+    const double bytes = 10.0 * 6 * HW + 2.0 * sp.feat_hist * sp.feat_len * 4 + 2.0 * sp.feat_len * 4;
+    add("inputs", "policy_inputs", 0, bytes, [=](hipStream_t s) {
+      launch_policy_inputs(q, warped, packed, counter, ring, fr, dr, img, fb, tail, s);
+    });
+  }
+  // 2. conv stem: im2col with zero-border image reads + MFMA GEMM, both streams batched
+  {
+    int H = sp.img_h, W = sp.img_w, C = 6 * sp.n_frames;
+    for (size_t i = 0; i < sp.stem.size(); ++i) {
+      const std::string si = std::to_string(i);
+      const int Co = sp.stem[i];
+      const int Ho = (H - 1) / 2 + 1, Wo = (W - 1) / 2 + 1;
+      const int Kp = (int)round_up(9L * C, 64);
+      half_t* patches = h16("patches");
+      const double pbytes = 2.0 * Ho * Wo * Kp * 2;
+      if (i == 0) {
+        const uint8_t* img = static_cast<uint8_t*>(ptr("img"));
+        add("stem0.im2col", "im2col_u8", 0, pbytes + 2.0 * C * HW, [=](hipStream_t s) {
+          launch_im2col_u8(img, 2, C, H, W, patches, Kp, s);
+        });
+      } else {
+        const half_t* prev = h16("stem." + std::to_string(i - 1) + ".out");
+        add("stem" + si + ".im2col", "im2col_f16", 0, pbytes + 2.0 * H * W * C * 2, [=](hipStream_t s) {
+          launch_im2col_f16(prev, 2, C, H, W, patches, Kp, s);
+        });
+      }
+      GemmDesc g;
+      g.A = patches; g.lda = Kp; g.sA = (long)Ho * Wo * Kp;
+      g.B = h16("stem." + si + ".w"); g.ldb = Kp; g.sB = (long)Co * Kp;
+      g.C = ptr("stem." + si + ".out"); g.ldc = Co; g.sC = (long)Ho * Wo * Co;
+      g.bias = f32("stem." + si + ".b"); g.sBias = Co;
+      g.M = Ho * Wo; g.N = Co; g.K = Kp; g.batch = 2; g.epi = EPI_F16_BIAS_RELU;
+      add_gemm("stem" + si + ".conv", "gemm_conv_relu", g);
+      H = Ho; W = Wo; C = Co;
+    }
+  }
+  // 3. tokens, temporal context, embedding
+  {
+    const half_t* so = h16("stem." + std::to_string(sp.stem.size() - 1) + ".out");
+    half_t* tok = h16("tokens");
+    const int ns = n_spatial, C5 = T;
+    add("tokens", "tokens", 0, 2.0 * 2 * ns * C5 * 2, [=](hipStream_t s) { launch_tokens(so, ns, C5, tok, s); });
+    const int Kt = sp.feat_hist * sp.feat_len, Td = sp.temporal_dim;
+    const half_t* tw = h16("tmp.w");
+    const float* tb = f32("tmp.b");
+    const float* fbuf = f32("feat_buf");
+    float* cin = f32("ctx_in");
+    add("temporal", "gemv", 2.0 * Td * Kt, (double)Td * Kt * 2 + Kt * 4 + Td * 8, [=](hipStream_t s) {
+      launch_gemv(tw, fbuf, tb, cin, Td, Kt, Kt, GEMV_GELU, 0, s);
+    });
+    const half_t* cw = h16("ctx.w");
+    const float* cb = f32("ctx.b");
+    float* ctx = f32("ctx");
+    const int ldc = ld_ctx;
+    add("context", "gemv", 2.0 * d * ldc, (double)d * ldc * 2 + ldc * 4 + d * 8, [=](hipStream_t s) {
+      launch_gemv(cw, cin, cb, ctx, d, ldc, ldc, GEMV_NONE, 0, s);
+    });
+    const half_t* pos = h16("pos");
+    const float* eb = f32("emb.b");
+    float* x = f32("x");
+    const int Tt = T;
+    add("embed.init", "embed_init", 0, (double)Tt * d * 6 + d * 8, [=](hipStream_t s) {
+      launch_embed_init(pos, ctx, eb, x, Tt, d, s);
+    });
+    GemmDesc g;
+    g.A = tok; g.lda = 2 * ns;
+    g.B = h16("emb.w"); g.ldb = 2 * ns;
+    g.C = x; g.ldc = d;
+    g.M = T; g.N = d; g.K = 2 * ns; g.epi = EPI_F32_RESID;
+    add_gemm("embed", "gemm_resid", g);
+  }
+  // 4. transformer blocks
+  for (int l = 0; l < sp.n_layers; ++l) {
+    const std::string p = "blk." + std::to_string(l) + ".";
+    const std::string b = "blk" + std::to_string(l) + ".";
+    const float* x = f32("x");
+    half_t* hb = h16("h16");
+    const float* g1 = f32(p + "ln1.g");
+    const float* b1 = f32(p + "ln1.b");
+    const int Tt = T;
+    const float eps = sp.eps;
+    add(b + "ln1", "layernorm_f16", 0, (double)Tt * d * 6, [=](hipStream_t s) {
+      launch_layernorm(x, g1, b1, hb, true, Tt, d, eps, s);
+    });
+    GemmDesc q;
+    q.A = hb; q.lda = d; q.B = h16(p + "qkv.w"); q.ldb = d; q.C = ptr("qk"); q.ldc = 2 * d;
+    q.bias = f32(p + "qkv.b"); q.M = T; q.N = 3 * d; q.K = d; q.epi = EPI_QKV;
+    q.vt = h16("vt"); q.qk_cols = 2 * d; q.vt_ld = T;
+    add_gemm(b + "qkv", "gemm_qkv", q);
+    const half_t* qk = h16("qk");
+    const half_t* vt = h16("vt");
+    half_t* att = h16("att");
+    const int nh = sp.n_heads, hd = sp.head_dim;
+    add(b + "attn", "attention", 4.0 * Tt * Tt * d, (double)Tt * d * 2 * 4, [=](hipStream_t s) {
+      launch_attention(qk, vt, att, Tt, nh, hd, s);
+    });
+    GemmDesc o;
+    o.A = att; o.lda = d; o.B = h16(p + "o.w"); o.ldb = d; o.C = ptr("x"); o.ldc = d;
+    o.bias = f32(p + "o.b"); o.M = T; o.N = d; o.K = d; o.epi = EPI_F32_RESID;
+    add_gemm(b + "o", "gemm_resid", o);
+    const float* g2 = f32(p + "ln2.g");
+    const float* b2 = f32(p + "ln2.b");
+    add(b + "ln2", "layernorm_f16", 0, (double)Tt * d * 6, [=](hipStream_t s) {
+      launch_layernorm(x, g2, b2, hb, true, Tt, d, eps, s);
+    });
+    GemmDesc up;
+    up.A = hb; up.lda = d; up.B = h16(p + "up.w"); up.ldb = d; up.C = ptr("u"); up.ldc = F;
+    up.bias = f32(p + "up.b"); up.M = T; up.N = F; up.K = d; up.epi = EPI_F16_BIAS_GELU;
+    add_gemm(b + "up", "gemm_gelu", up);
+    GemmDesc dn;
+    dn.A = h16("u"); dn.lda = F; dn.B = h16(p + "down.w"); dn.ldb = F; dn.C = ptr("x"); dn.ldc = d;
+    dn.bias = f32(p + "down.b"); dn.M = T; dn.N = d; dn.K = F; dn.epi = EPI_F32_RESID;
+    add_gemm(b + "down", "gemm_resid", dn);
+  }
+  // 5. final LN + pool, GRU, heads, tick
+  {
+    const float* x = f32("x");
+    float* xf = f32("xf");
+    const float* gf = f32("lnf.g");
+    const float* bf = f32("lnf.b");
+    float* pooled = f32("pooled");
+    const int Tt = T;
+    const float eps = sp.eps;
+    add("final.ln", "layernorm_f32", 0, (double)Tt * d * 8, [=](hipStream_t s) {
+      launch_layernorm(x, gf, bf, xf, false, Tt, d, eps, s);
+    });
+    add("final.pool", "colmean", 0, (double)Tt * d * 4, [=](hipStream_t s) { launch_colmean(xf, pooled, Tt, d, s); });
+    const float* hprev = f32("packed") + dl + 4;
+    float* gi = f32("gi");
+    float* gh = f32("gh");
+    const half_t* wih = h16("gru.wih");
+    const half_t* whh = h16("gru.whh");
+    const float* bih = f32("gru.bih");
+    const float* bhh = f32("gru.bhh");
+    add("gru.ih", "gemv", 2.0 * 3 * Hh * d, 3.0 * Hh * d * 2, [=](hipStream_t s) {
+      launch_gemv(wih, pooled, bih, gi, 3 * Hh, d, d, GEMV_NONE, 0, s);
+    });
+    add("gru.hh", "gemv", 2.0 * 3 * Hh * Hh, 3.0 * Hh * Hh * 2, [=](hipStream_t s) {
+      launch_gemv(whh, hprev, bhh, gh, 3 * Hh, Hh, Hh, GEMV_NONE, 0, s);
+    });
+    float* out = f32("out");
+    float* hn = f32("h_new");
+    const int nho = n_head_out;
+    add("gru.gate", "gru_gate", 0, 8.0 * Hh * 4, [=](hipStream_t s) {
+      launch_gru_gate(gi, gh, hprev, hn, out + nho, Hh, s);
+    });
+    const half_t* hw = h16("head.w");
+    const float* hbias = f32("head.b");
+    add("heads", "gemv", 2.0 * nho * Hh, (double)nho * Hh * 2, [=](hipStream_t s) {
+      launch_gemv(hw, hn, hbias, out, nho, Hh, Hh, GEMV_NONE, 0, s);
+    });
+    unsigned* counter = static_cast<unsigned*>(ptr("counter"));
+    float* feat = f32("packed") + dl + 4;
+    add("tick", "frame_tick", 0, 8.0 * Hh, [=](hipStream_t s) { launch_frame_tick(counter, hn, feat, Hh, s); });
+  }
+  if (ws_floats) CK_HIP(hipMalloc((void**)&ws, ws_floats * sizeof(float)));
+}
+
+void ck_engine::upload(const std::string& name, const void* host, size_t nbytes) {
+  Tensor& t = tensor(name);
+  CK_REQUIRE(nbytes == t.nbytes, "upload " + name + ": expected " + std::to_string(t.nbytes) + " bytes, got " +
+                                     std::to_string(nbytes));
+  if (t.ld == t.cols) {
+    CK_HIP(hipMemcpy(t.ptr, host, nbytes, hipMemcpyHostToDevice));
+  } else {
+    const size_t esz = t.dtype == DT_F16 ? 2 : t.dtype == DT_U8 ? 1 : 4;
+    CK_HIP(hipMemcpy2D(t.ptr, t.ld * esz, host, t.cols * esz, t.cols * esz, t.rows, hipMemcpyHostToDevice));
+  }
+}
+
+void ck_engine::drop_graph() {
+  if (gexec) (void)hipGraphExecDestroy(gexec);
+  if (graph) (void)hipGraphDestroy(graph);
+  gexec = nullptr;
+  graph = nullptr;
+  graph_nodes = 0;
+}
+
+void ck_engine::capture() {
+  drop_graph();
+  CK_HIP(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal));
+  try {
+    for (auto& l : plan) l.fn(stream);
+  } catch (...) {
+    hipGraph_t g = nullptr;
+    (void)hipStreamEndCapture(stream, &g);
+    if (g) (void)hipGraphDestroy(g);
+    throw;
+  }
+  CK_HIP(hipStreamEndCapture(stream, &graph));
+  CK_HIP(hipGraphGetNodes(graph, nullptr, &graph_nodes));
+  CK_HIP(hipGraphInstantiate(&gexec, graph, nullptr, nullptr, 0));
+}
+
+void ck_engine::frame_launch() {
+  if (use_graph) {
+    if (!gexec) capture();
+    CK_HIP(hipGraphLaunch(gexec, stream));
+  } else {
+    for (auto& l : plan) l.fn(stream);
+  }
+}
+
+void ck_engine::run_frame(const uint8_t* warped, const float* packed, float* out) {
+  std::memcpy(h_warped, warped, warped_bytes);
+  std::memcpy(h_packed, packed, packed_len * sizeof(float));
+  CK_HIP(hipMemcpyAsync(ptr("warped"), h_warped, warped_bytes, hipMemcpyHostToDevice, stream));
+  CK_HIP(hipMemcpyAsync(ptr("packed"), h_packed, packed_len * sizeof(float), hipMemcpyHostToDevice, stream));
+  frame_launch();
+  CK_HIP(hipMemcpyAsync(h_out, ptr("out"), n_out * sizeof(float), hipMemcpyDeviceToHost, stream));
+  CK_HIP(hipStreamSynchronize(stream));
+  std::memcpy(out, h_out, n_out * sizeof(float));
+}
+
+void ck_engine::reset_state() {
+  for (const char* n : {"counter", "img_ring", "feat_ring", "desire_ring"}) {
+    Tensor& t = tensor(n);
+    launch_fill_u32(t.ptr, 0u, round_up((long)t.nbytes, 4) / 4, stream);
+  }
+  CK_HIP(hipStreamSynchronize(stream));
+}
+
+void ck_engine::run_range(int first, int last) {
+  CK_REQUIRE(first >= 0 && last <= (int)plan.size() && first <= last, "run_range: bad plan range");
+  for (int i = first; i < last; ++i) plan[i].fn(stream);
+  CK_HIP(hipStreamSynchronize(stream));
+}
+
+void ck_engine::kernel_times(float* ms, int n) {
+  CK_REQUIRE(n >= (int)plan.size(), "kernel_times: output array shorter than the plan");
+  hipEvent_t e0, e1;
+  CK_HIP(hipEventCreate(&e0));
+  CK_HIP(hipEventCreate(&e1));
+  try {
+    CK_HIP(hipStreamSynchronize(stream));
+    for (size_t i = 0; i < plan.size(); ++i) {
+      CK_HIP(hipEventRecord(e0, stream));
+      plan[i].fn(stream);
+      CK_HIP(hipEventRecord(e1, stream));
+      CK_HIP(hipEventSynchronize(e1));
+      CK_HIP(hipEventElapsedTime(&ms[i], e0, e1));
+    }
+  } catch (...) {
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    throw;
+  }
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+}
+
+float ck_engine::time_launches(const int* idx, int n, int reps) {
+  for (int i = 0; i < n; ++i)
+    CK_REQUIRE(idx[i] >= 0 && idx[i] < (int)plan.size(), "time_launches: plan index out of range");
+  hipEvent_t e0, e1;
+  CK_HIP(hipEventCreate(&e0));
+  CK_HIP(hipEventCreate(&e1));
+  float ms = 0.f;
+  try {
+    CK_HIP(hipStreamSynchronize(stream));
+    CK_HIP(hipEventRecord(e0, stream));
+    for (int r = 0; r < reps; ++r)
+      for (int i = 0; i < n; ++i) plan[idx[i]].fn(stream);
+    CK_HIP(hipEventRecord(e1, stream));
+    CK_HIP(hipEventSynchronize(e1));
+    CK_HIP(hipEventElapsedTime(&ms, e0, e1));
+  } catch (...) {
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    throw;
+  }
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  return ms;
+}

@@ -1,0 +1,91 @@
+// The per-frame engine: model spec, device tensors, the resolved frame plan
+// and its hipGraph.  Replaces the reference's L4/L5 layers: pickle decode +
+// queue allocation (run_pinned2.py:1346-1389) and the replay / CUDA-graph
+// frame executor (run_pinned2.py:1391-1572).
+#pragma once
+
+#include <functional>
+#include <map>
+#include <string>
+#include <vector>
+
+#include "common.h"
+#include "kernels.h"
+
+namespace ck {
+
+struct Spec {
+  std::string name;
+  int img_h = 128, img_w = 256, n_frames = 2, fs = 4;
+  int feat_len = 512, feat_hist = 24, desire_len = 8, desire_hist = 25;
+  int hidden = 512, d = 0, n_heads = 0, head_dim = 0, n_layers = 0, d_ff = 0, temporal_dim = 0;
+  float eps = 1e-5f;
+  std::vector<int> stem;
+  std::vector<std::pair<std::string, int>> outputs;
+};
+Spec parse_spec(const std::string& json);
+
+enum DType { DT_F32 = 0, DT_F16 = 1, DT_U8 = 2, DT_U32 = 3 };
+
+struct Tensor {
+  std::string name;
+  void* ptr = nullptr;
+  size_t nbytes = 0;     // logical bytes (what upload/read/write transfer)
+  int dtype = DT_F32;
+  long rows = 1, cols = 0, ld = 0;   // 2-D view for padded parameter layouts
+  bool param = false;
+};
+
+struct Launch {
+  std::string name;      // plan position, e.g. "blk3.qkv"
+  std::string kernel;    // kernel family, e.g. "gemm_qkv"
+  double flops = 0, bytes = 0;   // algorithmic work of one launch
+  std::function<void(hipStream_t)> fn;
+};
+
+}  // namespace ck
+
+struct ck_engine {
+  ck::Spec sp;
+  hipStream_t stream = nullptr;
+  std::vector<ck::Tensor> tensors;
+  std::map<std::string, size_t> by_name;
+  std::vector<ck::Launch> plan;
+  bool use_graph = true;
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t gexec = nullptr;
+  size_t graph_nodes = 0;
+  float* ws = nullptr;
+  size_t ws_floats = 0;
+  uint8_t* h_warped = nullptr;   // pinned staging (outlives every async copy)
+  float* h_packed = nullptr;
+  float* h_out = nullptr;
+  // derived sizes
+  int T = 0, n_spatial = 0, n_head_out = 0, n_out = 0, n_ctx = 0, ld_ctx = 0, packed_len = 0;
+  size_t warped_bytes = 0;
+
+  explicit ck_engine(const std::string& spec_json);
+  ~ck_engine();
+
+  ck::Tensor& tensor(const std::string& name);
+  void* ptr(const std::string& name) { return tensor(name).ptr; }
+  void upload(const std::string& name, const void* host, size_t nbytes);
+  void run_frame(const uint8_t* warped, const float* packed, float* out);
+  void frame_launch();
+  void capture();
+  void drop_graph();
+  void reset_state();
+  void run_range(int first, int last);
+  void kernel_times(float* ms, int n);
+  float time_launches(const int* idx, int n, int reps);
+
+ private:
+  ck::Tensor& add_tensor(const std::string& name, size_t nbytes, int dtype, bool param, long rows = 1, long cols = 0,
+                         long ld = 0);
+  void build_params();
+  void build_activations();
+  void build_plan();
+  void add(const std::string& name, const std::string& kernel, double flops, double bytes,
+           std::function<void(hipStream_t)> fn);
+  void add_gemm(const std::string& name, const std::string& kernel, ck::GemmDesc g);
+};

@@ -1,0 +1,345 @@
+// f16-input / f32-accumulate GEMM on gfx950 MFMA: the replacement of the
+// WMMA attention/projection kernels r_6_2, r_2_24, r_12_32_4, r_48_32_4
+// (run_pinned2.py:100-266, 866-934; NOTES.md:84-104).
+//
+// Those kernels are serial K loops whose whole output tile lives in the
+// register file as loop-carried fragments, one block per SM (255 registers).
+// This kernel instead:
+//   * stages A and B tiles (BK = 64) through LDS, double buffered, with
+//     rows padded to 72 halves so the 16-byte MFMA operand reads of 8
+//     consecutive lanes hit distinct banks;
+//   * computes with v_mfma_f32_32x32x16_f16 (wave64; a 2x2 wave grid, each
+//     wave owns a (BM/2)x(BN/2) sub-tile, at most 4 MFMA accumulators of 16
+//     floats);
+//   * splits K over extra workgroups when the output has too few tiles to
+//     fill 256 CUs (the graph-level split-K the reference names as its next
+//     lever, README.md:170-175), writing f32 partials that a second kernel
+//     sums in split order -- deterministic, unlike atomics;
+//   * orders tiles so that consecutive workgroup ids, which the dispatcher
+//     spreads round-robin over the 8 XCDs, are regrouped so each XCD gets a
+//     contiguous run of M-tiles sharing the same B (weight) columns in its L2;
+//   * fuses bias / ReLU / GELU / residual-add / QKV-split epilogues.
+// MFMA 32x32x16 operand layout (lane l of 64): A row l%32, k = 8*(l/32)..+7;
+// B column l%32, same k; D element e of lane l is row 8*(e/4) + 4*(l/32) +
+// e%4, column l%32.  The layout is checked by the MFMA KAT (wmma.hip).
+#include "common.h"
+#include "kernels.h"
+
+namespace ck {
+namespace {
+
+constexpr int BK = 64;
+constexpr int LDK = BK + 8;   // padded LDS row (halves)
+
+struct GemmParams {
+  const half_t* A;
+  const half_t* B;
+  void* C;
+  const float* bias;
+  float* ws;
+  half_t* vt;
+  long lda, ldb, ldc, vt_ld;
+  long sA, sB, sC, sBias;
+  int M, N, K, kps;   // kps: K per split
+  int split, batch, Mt, Nt;
+  int qk_cols;
+};
+
+template <int EPI>
+__device__ __forceinline__ void epi_store(const GemmParams& p, void* C, const float* bias, int m, int n, float v) {
+  if (EPI == EPI_F32) {
+    if (bias) v += bias[n];
+    static_cast<float*>(C)[(long)m * p.ldc + n] = v;
+  } else if (EPI == EPI_F32_RESID) {
+    if (bias) v += bias[n];
+    float* c = static_cast<float*>(C) + (long)m * p.ldc + n;
+    *c = *c + v;
+  } else {
+    if (bias) v += bias[n];
+    if (EPI == EPI_F16_BIAS_RELU) v = fmaxf(v, 0.f);
+    if (EPI == EPI_F16_BIAS_GELU) v = gelu_tanh(v);
+    if (EPI == EPI_QKV && n >= p.qk_cols) {
+      p.vt[(long)(n - p.qk_cols) * p.vt_ld + m] = (half_t)v;
+    } else {
+      static_cast<half_t*>(C)[(long)m * p.ldc + n] = (half_t)v;
+    }
+  }
+}
+
+// 8x8 transpose of f16 values held as 8 rows of 4 packed words.
+__device__ __forceinline__ void transpose8x8(const uint32_t (&in)[8][4], uint32_t (&out)[8][4]) {
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t a = in[2 * j][q], b = in[2 * j + 1][q];
+      out[2 * q][j] = (a & 0xFFFFu) | (b << 16);            // column 2q: low halves
+      out[2 * q + 1][j] = (a >> 16) | (b & 0xFFFF0000u);    // column 2q+1: high halves
+    }
+  }
+}
+
+template <int BM, int BN, bool BKN, int EPI>
+__global__ __launch_bounds__(256) void gemm_kernel(const GemmParams p) {
+  __shared__ __attribute__((aligned(16))) half_t As[2][BM][LDK];
+  __shared__ __attribute__((aligned(16))) half_t Bs[2][BN][LDK];
+
+  constexpr int WM = BM / 2, WN = BN / 2;   // wave sub-tile
+  constexpr int FM = WM / 32, FN = WN / 32;
+  constexpr int ACH = BM * BK / 8 / 256;    // 16-byte A chunks per thread
+  constexpr int BCH = BN * BK / 8 / 256;    // 16-byte B chunks per thread (NK layout)
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+
+  // ---- tile decode (XCD-grouped) ----
+  const int total = p.Mt * p.Nt * p.split * p.batch;
+  int L = blockIdx.x;
+  if ((total & 7) == 0) L = (L & 7) * (total >> 3) + (L >> 3);
+  const int mt = L % p.Mt; L /= p.Mt;
+  const int nt = L % p.Nt; L /= p.Nt;
+  const int sp = L % p.split;
+  const int bz = L / p.split;
+
+  const half_t* A = p.A + bz * p.sA;
+  const half_t* B = p.B + bz * p.sB;
+  const int m0 = mt * BM, n0 = nt * BN;
+  const int kbeg = sp * p.kps;
+  const int nk = p.kps / BK;
+
+  // ---- global -> register loaders ----
+  half8_t ra[ACH];
+  half8_t rb[BKN ? 8 : BCH];
+  auto load_tiles = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < ACH; ++i) {
+      const int c = tid + 256 * i, row = c >> 3, kc = (c & 7) * 8;
+      const int gm = min(m0 + row, p.M - 1);
+      ra[i] = *reinterpret_cast<const half8_t*>(A + (long)gm * p.lda + k0 + kc);
+    }
+    if (!BKN) {
+#pragma unroll
+      for (int i = 0; i < BCH; ++i) {
+        const int c = tid + 256 * i, row = c >> 3, kc = (c & 7) * 8;
+        const int gn = min(n0 + row, p.N - 1);
+        rb[i] = *reinterpret_cast<const half8_t*>(B + (long)gn * p.ldb + k0 + kc);
+      }
+    } else if (tid < BN) {
+      // B is [K][N]: thread loads an 8(k) x 8(n) block, transposed on store
+      const int kb = tid / (BN / 8), nb = tid % (BN / 8);
+      const int gn = min(n0 + nb * 8, p.N - 8);
+#pragma unroll
+      for (int r = 0; r < 8; ++r)
+        rb[r] = *reinterpret_cast<const half8_t*>(B + (long)(k0 + kb * 8 + r) * p.ldb + gn);
+    }
+  };
+  auto store_tiles = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < ACH; ++i) {
+      const int c = tid + 256 * i, row = c >> 3, kc = (c & 7) * 8;
+      *reinterpret_cast<half8_t*>(&As[buf][row][kc]) = ra[i];
+    }
+    if (!BKN) {
+#pragma unroll
+      for (int i = 0; i < BCH; ++i) {
+        const int c = tid + 256 * i, row = c >> 3, kc = (c & 7) * 8;
+        *reinterpret_cast<half8_t*>(&Bs[buf][row][kc]) = rb[i];
+      }
+    } else if (tid < BN) {
+      const int kb = tid / (BN / 8), nb = tid % (BN / 8);
+      uint32_t in[8][4], out[8][4];
+#pragma unroll
+      for (int r = 0; r < 8; ++r) {
+        const uint32_t* w = reinterpret_cast<const uint32_t*>(&rb[r]);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) in[r][q] = w[q];
+      }
+      transpose8x8(in, out);
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        uint32_t* dst = reinterpret_cast<uint32_t*>(&Bs[buf][nb * 8 + c][kb * 8]);
+        dst[0] = out[c][0]; dst[1] = out[c][1]; dst[2] = out[c][2]; dst[3] = out[c][3];
+      }
+    }
+  };
+
+  float16_t acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = float16_t{};
+
+  load_tiles(kbeg);
+  store_tiles(0);
+  __syncthreads();
+
+  for (int it = 0; it < nk; ++it) {
+    const int buf = it & 1;
+    if (it + 1 < nk) load_tiles(kbeg + (it + 1) * BK);
+#pragma unroll
+    for (int kk = 0; kk < BK; kk += 16) {
+      half8_t af[FM], bf[FN];
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+        af[i] = *reinterpret_cast<const half8_t*>(&As[buf][wm * WM + i * 32 + (lane & 31)][kk + (lane >> 5) * 8]);
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+        bf[j] = *reinterpret_cast<const half8_t*>(&Bs[buf][wn * WN + j * 32 + (lane & 31)][kk + (lane >> 5) * 8]);
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+    }
+    if (it + 1 < nk) {
+      store_tiles(buf ^ 1);
+      __syncthreads();
+    }
+  }
+
+  // ---- epilogue ----
+  if (p.split > 1) {
+    float* ws = p.ws + ((long)sp * p.batch + bz) * (long)p.M * p.N;
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int m = m0 + wm * WM + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+          const int n = n0 + wn * WN + j * 32 + (lane & 31);
+          if (m < p.M && n < p.N) ws[(long)m * p.N + n] = acc[i][j][e];
+        }
+    return;
+  }
+  void* C = (EPI == EPI_F32 || EPI == EPI_F32_RESID)
+                ? static_cast<void*>(static_cast<float*>(p.C) + bz * p.sC)
+                : static_cast<void*>(static_cast<half_t*>(p.C) + bz * p.sC);
+  const float* bias = p.bias ? p.bias + bz * p.sBias : nullptr;
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int m = m0 + wm * WM + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+        const int n = n0 + wn * WN + j * 32 + (lane & 31);
+        if (m < p.M && n < p.N) epi_store<EPI>(p, C, bias, m, n, acc[i][j][e]);
+      }
+}
+
+// Sums split-K partials in split order, then applies the epilogue.
+template <int EPI>
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const GemmParams p) {
+  const long MN = (long)p.M * p.N;
+  const long idx = (long)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= MN * p.batch) return;
+  const int bz = (int)(idx / MN);
+  const long r = idx - bz * MN;
+  const int m = (int)(r / p.N), n = (int)(r - (long)m * p.N);
+  float v = 0.f;
+  for (int s = 0; s < p.split; ++s) v += p.ws[((long)s * p.batch + bz) * MN + r];
+  void* C = (EPI == EPI_F32 || EPI == EPI_F32_RESID)
+                ? static_cast<void*>(static_cast<float*>(p.C) + bz * p.sC)
+                : static_cast<void*>(static_cast<half_t*>(p.C) + bz * p.sC);
+  const float* bias = p.bias ? p.bias + bz * p.sBias : nullptr;
+  epi_store<EPI>(p, C, bias, m, n, v);
+}
+
+template <int BM, int BN, bool BKN, int EPI>
+void launch_tile(const GemmParams& p, hipStream_t s) {
+  const int grid = p.Mt * p.Nt * p.split * p.batch;
+  hipLaunchKernelGGL((gemm_kernel<BM, BN, BKN, EPI>), dim3(grid), dim3(256), 0, s, p);
+  CK_LAUNCHED("gemm");
+}
+
+template <bool BKN, int EPI>
+void launch_epi(int tile, const GemmParams& p, hipStream_t s) {
+  switch (tile) {
+    case 1: launch_tile<128, 128, BKN, EPI>(p, s); break;
+    case 2: launch_tile<128, 64, BKN, EPI>(p, s); break;
+    case 3: launch_tile<64, 128, BKN, EPI>(p, s); break;
+    default: launch_tile<64, 64, BKN, EPI>(p, s); break;
+  }
+}
+
+template <int EPI>
+void launch_reduce(const GemmParams& p, hipStream_t s) {
+  const long n = (long)p.M * p.N * p.batch;
+  hipLaunchKernelGGL(splitk_reduce_kernel<EPI>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, p);
+  CK_LAUNCHED("splitk_reduce");
+}
+
+int tile_bm(int tile) { return (tile == 1 || tile == 2) ? 128 : 64; }
+int tile_bn(int tile) { return (tile == 1 || tile == 3) ? 128 : 64; }
+
+}  // namespace
+
+size_t gemm_plan(GemmDesc& d) {
+  CK_REQUIRE(d.M > 0 && d.N > 0 && d.K > 0 && d.batch > 0, "gemm: empty problem");
+  CK_REQUIRE(d.K % BK == 0, "gemm: K must be a multiple of 64 (pad K)");
+  if (d.tile == 0) {
+    // 128-wide tiles unless a dimension is small; 64x64 when even split-K
+    // cannot give the 256 CUs enough workgroups with 128x128 tiles.
+    int bm = d.M <= 64 ? 64 : 128, bn = d.N <= 64 ? 64 : 128;
+    const long t = (long)ceil_div(d.M, bm) * ceil_div(d.N, bn) * d.batch;
+    if (t < 64 && d.K < 1024) bm = bn = 64;
+    if (d.b_kn) bn = 128;
+    d.tile = bm == 128 ? (bn == 128 ? 1 : 2) : (bn == 128 ? 3 : 4);
+  }
+  CK_REQUIRE(d.tile >= 1 && d.tile <= 4, "gemm: unknown tile code");
+  if (d.b_kn) CK_REQUIRE(d.tile == 1 || d.tile == 3, "gemm: [K][N] B needs a 128-wide N tile");
+  const long tiles = (long)ceil_div(d.M, tile_bm(d.tile)) * ceil_div(d.N, tile_bn(d.tile)) * d.batch;
+  if (d.split == 0) {
+    // split K only while the grid stays within one wave of 256 CUs
+    int s = 1;
+    while (s < 8 && tiles * s * 2 <= 256 && d.K % (BK * s * 2) == 0 && d.K / (s * 2) >= 512) s *= 2;
+    d.split = s;
+  }
+  CK_REQUIRE(d.split >= 1 && d.K % (BK * d.split) == 0, "gemm: K must split into multiples of 64");
+  return d.split > 1 ? (size_t)d.split * d.batch * d.M * d.N : 0;
+}
+
+void launch_gemm(GemmDesc d, hipStream_t s) {
+  const size_t need = gemm_plan(d);
+  CK_REQUIRE(d.A && d.B && d.C, "gemm: null operand");
+  CK_REQUIRE(d.lda >= d.K && d.lda % 8 == 0, "gemm: lda must be >= K and a multiple of 8");
+  if (d.b_kn) {
+    CK_REQUIRE(d.ldb >= d.N && d.ldb % 8 == 0 && d.N % 8 == 0, "gemm: [K][N] B needs N, ldb multiples of 8");
+    CK_REQUIRE(d.epi == EPI_F32, "gemm: [K][N] B supports the f32 epilogue only");
+  } else {
+    CK_REQUIRE(d.ldb >= d.K && d.ldb % 8 == 0, "gemm: ldb must be >= K and a multiple of 8");
+  }
+  // QKV: only the first qk_cols columns are stored row-major in C
+  CK_REQUIRE(d.ldc >= (d.epi == EPI_QKV ? d.qk_cols : d.N), "gemm: ldc must be >= N (>= qk_cols for QKV)");
+  CK_REQUIRE((reinterpret_cast<uintptr_t>(d.A) & 15) == 0 && (reinterpret_cast<uintptr_t>(d.B) & 15) == 0,
+             "gemm: A and B must be 16-byte aligned");
+  CK_REQUIRE(d.sA % 8 == 0 && d.sB % 8 == 0, "gemm: batch strides must keep 16-byte alignment");
+  if (d.epi == EPI_QKV) CK_REQUIRE(d.vt && d.qk_cols > 0 && d.qk_cols < d.N && d.vt_ld >= d.M, "gemm: bad QKV split");
+  if (need) CK_REQUIRE(d.ws && d.ws_floats >= need, "gemm: split-K workspace missing or too small");
+  CK_REQUIRE((long)d.M * d.lda < (1L << 31) * 8, "gemm: A too large");
+
+  GemmParams p;
+  p.A = d.A; p.B = d.B; p.C = d.C; p.bias = d.bias; p.ws = d.ws; p.vt = d.vt;
+  p.lda = d.lda; p.ldb = d.ldb; p.ldc = d.ldc; p.vt_ld = d.vt_ld;
+  p.sA = d.sA; p.sB = d.sB; p.sC = d.sC; p.sBias = d.sBias;
+  p.M = d.M; p.N = d.N; p.K = d.K; p.split = d.split; p.kps = d.K / d.split; p.batch = d.batch;
+  p.Mt = ceil_div(d.M, tile_bm(d.tile)); p.Nt = ceil_div(d.N, tile_bn(d.tile));
+  p.qk_cols = d.qk_cols;
+  if (d.b_kn) {
+    launch_epi<true, EPI_F32>(d.tile, p, s);
+    if (d.split > 1) launch_reduce<EPI_F32>(p, s);
+    return;
+  }
+  switch (d.epi) {
+    case EPI_F32: launch_epi<false, EPI_F32>(d.tile, p, s); if (d.split > 1) launch_reduce<EPI_F32>(p, s); break;
+    case EPI_F16_BIAS: launch_epi<false, EPI_F16_BIAS>(d.tile, p, s); if (d.split > 1) launch_reduce<EPI_F16_BIAS>(p, s); break;
+    case EPI_F16_BIAS_RELU: launch_epi<false, EPI_F16_BIAS_RELU>(d.tile, p, s); if (d.split > 1) launch_reduce<EPI_F16_BIAS_RELU>(p, s); break;
+    case EPI_F16_BIAS_GELU: launch_epi<false, EPI_F16_BIAS_GELU>(d.tile, p, s); if (d.split > 1) launch_reduce<EPI_F16_BIAS_GELU>(p, s); break;
+    case EPI_F32_RESID: launch_epi<false, EPI_F32_RESID>(d.tile, p, s); if (d.split > 1) launch_reduce<EPI_F32_RESID>(p, s); break;
+    case EPI_QKV: launch_epi<false, EPI_QKV>(d.tile, p, s); if (d.split > 1) launch_reduce<EPI_QKV>(p, s); break;
+    default: throw Error("gemm: unknown epilogue");
+  }
+}
+
+}  // namespace ck

@@ -1,0 +1,103 @@
+// Host-side launchers for every device kernel of the frame.  All launchers
+// validate shapes/alignment on the host before launching (a bad shape is an
+// ck::Error, never an out-of-bounds access) and enqueue on the given stream.
+#pragma once
+
+#include "common.h"
+
+namespace ck {
+
+// ---- GEMV (serial reduce r_32_32_3_12288_32 analogue) ----------------------
+// y[r] = act(sum_k W[r*ldw + k] * x[k] + bias[r]),  r < rows, k < K.
+// W f16 row-major, x f32, y f32.  K % 8 == 0, ldw % 8 == 0, K <= 16384,
+// W and x 16-byte aligned.  act: 0 none, 1 gelu(tanh).  rows_per_wg: 0 = auto.
+enum GemvAct { GEMV_NONE = 0, GEMV_GELU = 1 };
+void launch_gemv(const half_t* W, const float* x, const float* bias, float* y, int rows, int K,
+                 int ldw, int act, int rows_per_wg, hipStream_t s);
+
+// ---- MFMA GEMM (WMMA attention/projection GEMM analogue) -------------------
+enum Epi {
+  EPI_F32 = 0,            // C32 = acc (+ bias)
+  EPI_F16_BIAS = 1,       // C16 = f16(acc + bias)
+  EPI_F16_BIAS_RELU = 2,  // C16 = f16(relu(acc + bias))
+  EPI_F16_BIAS_GELU = 3,  // C16 = f16(gelu(acc + bias))
+  EPI_F32_RESID = 4,      // C32 += acc (+ bias)
+  EPI_QKV = 5,            // f16(acc + bias): n < qk_cols -> C16[m][n], else vt[n-qk_cols][m]
+};
+
+struct GemmDesc {
+  const half_t* A = nullptr;   // [M][K] row-major, lda
+  const half_t* B = nullptr;   // [N][K] row-major (b_kn=false) or [K][N] (b_kn=true), ldb
+  void* C = nullptr;           // [M][N] row-major, ldc (f32 or f16 per epi)
+  const float* bias = nullptr; // [N] or null
+  long lda = 0, ldb = 0, ldc = 0;
+  int M = 0, N = 0, K = 0;
+  bool b_kn = false;
+  int epi = EPI_F32;
+  int split = 0;               // split-K factor; 0 = auto
+  float* ws = nullptr;         // split-K partials: split * batch * M * N floats
+  size_t ws_floats = 0;
+  int batch = 1;
+  long sA = 0, sB = 0, sC = 0, sBias = 0;   // per-batch element strides
+  half_t* vt = nullptr;        // EPI_QKV transposed V output
+  int qk_cols = 0;
+  long vt_ld = 0;
+  int tile = 0;                // 0 auto; else 1:128x128 2:128x64 3:64x128 4:64x64
+};
+// Resolves auto tile/split (writes them back) and returns the workspace the
+// launch needs, in floats.
+size_t gemm_plan(GemmDesc& d);
+void launch_gemm(GemmDesc d, hipStream_t s);
+
+// ---- attention ---------------------------------------------------------------
+// qk f16 [T][2d] (q | k, head h at columns h*hd), vt f16 [d][T] (V transposed),
+// out f16 [T][d].  Non-causal softmax(q k^T * scale) v per head.
+void launch_attention(const half_t* qk, const half_t* vt, half_t* out, int T, int n_heads, int head_dim,
+                      hipStream_t s);
+
+// ---- normalisation / small elementwise ---------------------------------------
+void launch_layernorm(const float* x, const float* g, const float* b, void* out, bool out_f16, int rows,
+                      int d, float eps, hipStream_t s);
+void launch_colmean(const float* x, float* out, int rows, int d, hipStream_t s);
+void launch_gru_gate(const float* gi, const float* gh, const float* h_prev, float* h_out, float* h_out2,
+                     int H, hipStream_t s);
+void launch_embed_init(const half_t* pos, const float* ctx, const float* bias, float* X, int T, int d,
+                       hipStream_t s);
+void launch_frame_tick(unsigned* counter, const float* h, float* packed_feat, int H, hipStream_t s);
+void launch_fill_u32(void* p, unsigned v, size_t n_words, hipStream_t s);
+
+// ---- frame inputs, packing, image2d ------------------------------------------
+struct QueueDims {
+  int img_h, img_w;          // 128, 256
+  int fs;                    // frame skip (4)
+  int img_slots;             // fs*(n_frames-1)+1 (5)
+  int feat_len, feat_hist;   // 512, 24
+  int desire_len, desire_hist;  // 8, 25
+};
+// One `run_policy` input stage on device ring buffers (see pack.hip).
+void launch_policy_inputs(const QueueDims& q, const uint8_t* warped, const float* packed, const unsigned* counter,
+                          uint8_t* img_ring, float* feat_ring, float* desire_ring, uint8_t* img_out,
+                          float* feat_out, float* ctx_tail, hipStream_t s);
+void launch_yuv_to_channels(const uint8_t* Y, const uint8_t* U, const uint8_t* V, int H, int W, uint8_t* out,
+                            hipStream_t s);
+void launch_i420_to_channels(const uint8_t* frame, int H, int W, uint8_t* out, hipStream_t s);
+// Zero-border gather: img has A rows of B texels of `lanes` elements of
+// `elem_bytes` bytes; yx int32 [n][2]; out [n][lanes].
+void launch_img_gather(const void* img, int A, int B, int lanes, int elem_bytes, const int* yx, int n, void* out,
+                       hipStream_t s);
+// Conv stem im2col (zero-border reads).  Layer 1 reads normalised uint8
+// planes [batch][C][H][W]; later layers read f16 [batch][H][W][C] texels.
+void launch_im2col_u8(const uint8_t* img, int batch, int C, int H, int W, half_t* patches, int Kp, hipStream_t s);
+void launch_im2col_f16(const half_t* act, int batch, int C, int H, int W, half_t* patches, int Kp, hipStream_t s);
+void launch_tokens(const half_t* stem_out, int n_spatial, int C5, half_t* F, hipStream_t s);
+
+// ---- KATs --------------------------------------------------------------------
+// RDNA4 wave32 WMMA fragments (u16 [32][8] A, B; f32 [32][8] C) -> D fragment,
+// computed on gfx950 MFMA.  n_tiles independent WMMAs.
+void launch_wmma_rdna4(const uint16_t* fa, const uint16_t* fb, const float* fc, float* fd, int n_tiles,
+                       hipStream_t s);
+// One MFMA on plain row-major operands: variant 0 = 16x16x32 f16, 1 = 32x32x16 f16.
+// A [M][K], B [K][N] (u16 f16 bits), D f32 [M][N].
+void launch_mfma_kat(int variant, const uint16_t* A, const uint16_t* B, float* D, hipStream_t s);
+
+}  // namespace ck

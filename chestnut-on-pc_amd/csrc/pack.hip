@@ -1,0 +1,319 @@
+// Integer-exact input-side kernels: policy input queues, uint8 frame packing,
+// image2d zero-border gathers and the conv-stem im2col built on them.
+#include "common.h"
+#include "kernels.h"
+
+namespace ck {
+namespace {
+
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ int wrap(long f, int n) {
+  long r = f % n;
+  return (int)(r < 0 ? r + n : r);
+}
+
+// ---------------------------------------------------------------------------
+// Policy input queues on ring buffers.
+//
+// The reference shifts every queue by one entry per frame and samples it
+// (shift_and_sample / sample_skip / sample_desire, compile_modeld.py:166-176,
+// called from run_policy, compile_modeld.py:198-212).  Here each queue is a
+// ring indexed by the device frame counter n (frames pushed so far), so no
+// entry is ever moved.  After the push of frame n the reference's queue
+// position j of a length-L queue holds the entry of frame n-L+1+j, which
+// lives in ring slot (n-L+1+j) mod L; slots never written are still zero, as
+// the reference's zero-initialised queues are.  The entry of frame n itself
+// is read from the input staging, never from the slot written in this same
+// launch, so no workgroup depends on another's store.
+//   img:    L = 5,   sample j = 0, 4        -> frames n-4 and n
+//   feat:   L = 96,  sample j = 0, 4, .., 92 -> frames n-95+4i (never n)
+//   desire: L = 100, group g = max over j = 4g..4g+3 (frame n in group 24)
+// ---------------------------------------------------------------------------
+struct PolicyArgs {
+  const uint8_t* warped;   // [2][6][H][W]
+  const float* packed;     // desire | tc2 | action_t2 | prev_feat
+  const unsigned* counter;
+  uint8_t* img_ring;       // [2][img_slots][6][H][W]
+  float* feat_ring;        // [fs*feat_hist][feat_len]
+  float* desire_ring;      // [fs*desire_hist][desire_len]
+  uint8_t* img_out;        // [2][6*n_frames][H][W]
+  float* feat_out;         // [feat_hist][feat_len]
+  float* ctx_tail;         // desire_pulse [desire_hist*desire_len] | tc2 | action_t2
+  int frame_units;         // 16-byte units per 6-channel frame
+  int img_slots, fs, feat_len, feat_hist, desire_len, desire_hist;
+  int n_img, n_feat, n_feat_push, n_des, n_des_push;   // work-range sizes
+};
+
+__global__ __launch_bounds__(256) void policy_inputs_kernel(const PolicyArgs a) {
+  long i = (long)blockIdx.x * 256 + threadIdx.x;
+  const long n = a.counter[0];
+  if (i < a.n_img) {   // two streams x frame_units: sample frames n-4 (ring) and n (staging); push n
+    const int s = (int)(i / a.frame_units), u = (int)(i % a.frame_units);
+    const long fb = (long)a.frame_units * 16;
+    const u32x4_t cur = reinterpret_cast<const u32x4_t*>(a.warped + s * fb)[u];
+    const int old_slot = wrap(n - (a.img_slots - 1), a.img_slots);
+    const int new_slot = wrap(n, a.img_slots);
+    uint8_t* ring = a.img_ring + (long)s * a.img_slots * fb;
+    const u32x4_t old = reinterpret_cast<const u32x4_t*>(ring + old_slot * fb)[u];
+    uint8_t* out = a.img_out + (long)s * 2 * fb;
+    reinterpret_cast<u32x4_t*>(out)[u] = old;
+    reinterpret_cast<u32x4_t*>(out + fb)[u] = cur;
+    reinterpret_cast<u32x4_t*>(ring + new_slot * fb)[u] = cur;
+    return;
+  }
+  i -= a.n_img;
+  const int fL = a.fs * a.feat_hist;
+  const float* prev_feat = a.packed + a.desire_len + 4;
+  if (i < a.n_feat) {   // feat_hist x feat_len samples
+    const int k = (int)(i / a.feat_len), c = (int)(i % a.feat_len);
+    const int slot = wrap(n - (fL - 1) + (long)a.fs * k, fL);
+    a.feat_out[i] = a.feat_ring[(long)slot * a.feat_len + c];
+    return;
+  }
+  i -= a.n_feat;
+  if (i < a.n_feat_push) {
+    a.feat_ring[(long)wrap(n, fL) * a.feat_len + i] = prev_feat[i];
+    return;
+  }
+  i -= a.n_feat_push;
+  const int dL = a.fs * a.desire_hist;
+  if (i < a.n_des) {   // desire_hist x desire_len group maxima
+    const int g = (int)(i / a.desire_len), c = (int)(i % a.desire_len);
+    float m = 0.f;
+    for (int t = 0; t < a.fs; ++t) {
+      const int j = g * a.fs + t;
+      const long f = n - (dL - 1) + j;
+      const float v = (j == dL - 1) ? a.packed[c] : a.desire_ring[(long)wrap(f, dL) * a.desire_len + c];
+      m = (t == 0 || v > m) ? v : m;
+    }
+    a.ctx_tail[i] = m;
+    return;
+  }
+  i -= a.n_des;
+  if (i < a.n_des_push) {
+    a.desire_ring[(long)wrap(n, dL) * a.desire_len + i] = a.packed[i];
+    return;
+  }
+  i -= a.n_des_push;
+  if (i < 4) a.ctx_tail[a.desire_hist * a.desire_len + i] = a.packed[a.desire_len + i];   // tc2 | action_t2
+}
+
+// ---------------------------------------------------------------------------
+// uint8 frame packing.
+// ---------------------------------------------------------------------------
+// [Y00, Y10, Y01, Y11, U00, V00] from full-resolution planes
+// (video_check.py:27-32).  Thread per output pixel.
+__global__ __launch_bounds__(256) void yuv_to_channels_kernel(const uint8_t* __restrict__ Y, const uint8_t* __restrict__ U,
+                                                              const uint8_t* __restrict__ V, int H, int W,
+                                                              uint8_t* __restrict__ out) {
+  const int h2 = H / 2, w2 = W / 2;
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (long)h2 * w2) return;
+  const int r = (int)(i / w2), c = (int)(i % w2);
+  const long plane = (long)h2 * w2;
+  const long y0 = (long)(2 * r) * W + 2 * c, y1 = y0 + W;
+  out[i] = Y[y0];
+  out[plane + i] = Y[y1];
+  out[2 * plane + i] = Y[y0 + 1];
+  out[3 * plane + i] = Y[y1 + 1];
+  out[4 * plane + i] = U[y0];
+  out[5 * plane + i] = V[y0];
+}
+
+// frames_to_tensor (compile_modeld.py:83-92): I420 [H*3/2][W] -> [6][H/2][W/2].
+// The U and V planes are contiguous runs of H/4 full rows, i.e. H*W/4 bytes
+// each, read in order as [H/2][W/2].
+__global__ __launch_bounds__(256) void i420_to_channels_kernel(const uint8_t* __restrict__ f, int H, int W,
+                                                               uint8_t* __restrict__ out) {
+  const int h2 = H / 2, w2 = W / 2;
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (long)h2 * w2) return;
+  const int r = (int)(i / w2), c = (int)(i % w2);
+  const long plane = (long)h2 * w2;
+  const long y0 = (long)(2 * r) * W + 2 * c, y1 = y0 + W;
+  out[i] = f[y0];
+  out[plane + i] = f[y1];
+  out[2 * plane + i] = f[y0 + 1];
+  out[3 * plane + i] = f[y1 + 1];
+  out[4 * plane + i] = f[(long)H * W + i];
+  out[5 * plane + i] = f[(long)H * W + plane + i];
+}
+
+// ---------------------------------------------------------------------------
+// image2d zero-border gather (run_pinned2.py:56-84, 355-374).
+// ---------------------------------------------------------------------------
+template <typename TexelT>
+__global__ __launch_bounds__(256) void img_gather_kernel(const TexelT* __restrict__ img, int A, int B,
+                                                         const int* __restrict__ yx, int n, TexelT* __restrict__ out) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  out[i] = img_texel_zb(img, A, B, yx[2 * i], yx[2 * i + 1]);
+}
+
+template <int LANES, typename E>
+struct alignas(sizeof(E) * LANES) Texel {
+  E v[LANES];
+};
+
+template <typename TexelT>
+void gather_launch(const void* img, int A, int B, const int* yx, int n, void* out, hipStream_t s) {
+  hipLaunchKernelGGL(img_gather_kernel<TexelT>, dim3(ceil_div(n, 256)), dim3(256), 0, s,
+                     static_cast<const TexelT*>(img), A, B, yx, n, static_cast<TexelT*>(out));
+  CK_LAUNCHED("img_gather");
+}
+
+// ---------------------------------------------------------------------------
+// Conv-stem im2col.  Patch row p = (ho, wo) of a 3x3 stride-2 pad-1 conv,
+// column k = (ky*3 + kx)*C + c, zero-padded to Kp columns.  Every input read
+// is an image2d texel read with a zero border.
+// ---------------------------------------------------------------------------
+// Layer 1: uint8 planes [batch][C][H][W], each plane an image of A=H rows of
+// B=W one-byte texels; value (u8 - 128) / 128, zero outside the image.
+__global__ __launch_bounds__(256) void im2col_u8_kernel(const uint8_t* __restrict__ img, int C, int H, int W,
+                                                        half_t* __restrict__ patches, int Kp, int Ho, int Wo) {
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  const long per = (long)Ho * Wo * Kp;
+  const int b = blockIdx.y;
+  if (i >= per) return;
+  const int k = (int)(i % Kp);
+  const long p = i / Kp;
+  half_t v = (half_t)0.f;
+  if (k < 9 * C) {
+    const int tap = k / C, c = k % C;
+    const int ho = (int)(p / Wo), wo = (int)(p % Wo);
+    const int y = 2 * ho - 1 + tap / 3, x = 2 * wo - 1 + tap % 3;
+    const uint8_t* plane = img + ((long)b * C + c) * H * W;
+    const int fl = y * W + x;
+    const int fc = min(max(fl, 0), H * W - 1);
+    const bool valid = (x >= 0) & (x < W) & (y >= 0) & (y < H);
+    const uint8_t u = plane[fc];
+    v = valid ? (half_t)(((float)u - 128.0f) * 0.0078125f) : (half_t)0.f;
+  }
+  patches[(long)b * per + i] = v;
+}
+
+// Later layers: f16 activations [batch][H][W][C] = an image of A=H rows of
+// B=W*C/4 texels of 4 halves.  Thread per 4-column texel of the patch row.
+__global__ __launch_bounds__(256) void im2col_f16_kernel(const half_t* __restrict__ act, int C, int H, int W,
+                                                         half_t* __restrict__ patches, int Kp, int Ho, int Wo) {
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  const int kq = Kp / 4;
+  const long per = (long)Ho * Wo * kq;
+  const int b = blockIdx.y;
+  if (i >= per) return;
+  const int k = (int)(i % kq) * 4;
+  const long p = i / kq;
+  u32x2_t v = {0u, 0u};
+  if (k < 9 * C) {
+    const int tap = k / C, c = k % C;
+    const int ho = (int)(p / Wo), wo = (int)(p % Wo);
+    const int y = 2 * ho - 1 + tap / 3, xs = 2 * wo - 1 + tap % 3;
+    const int B = W * (C / 4);
+    // texel column: xs = -1 gives x in [-C/4, 0), xs = W gives x >= B, so the
+    // zero-border rule alone supplies the conv padding
+    const int x = xs * (C / 4) + c / 4;
+    const u32x2_t* im = reinterpret_cast<const u32x2_t*>(act + (long)b * H * W * C);
+    v = img_texel_zb(im, H, B, y, x);
+  }
+  reinterpret_cast<u32x2_t*>(patches + (long)b * Ho * Wo * Kp)[i] = v;
+}
+
+// Channels-as-tokens: F[c][s*NS + p] = stem_out[s][p][c].
+__global__ __launch_bounds__(256) void tokens_kernel(const half_t* __restrict__ so, int NS, int C5,
+                                                     half_t* __restrict__ F) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= 2 * NS * C5) return;
+  const int c = i / (2 * NS), j = i % (2 * NS);
+  const int s = j / NS, p = j % NS;
+  F[i] = so[((long)s * NS + p) * C5 + c];
+}
+
+}  // namespace
+
+void launch_policy_inputs(const QueueDims& q, const uint8_t* warped, const float* packed, const unsigned* counter,
+                          uint8_t* img_ring, float* feat_ring, float* desire_ring, uint8_t* img_out, float* feat_out,
+                          float* ctx_tail, hipStream_t s) {
+  const long frame_bytes = 6L * q.img_h * q.img_w;
+  CK_REQUIRE(frame_bytes % 16 == 0, "policy_inputs: frame size must be a multiple of 16 bytes");
+  CK_REQUIRE(q.img_slots == q.fs + 1, "policy_inputs: two sampled frames expected (fs*(2-1)+1 slots)");
+  PolicyArgs a;
+  a.warped = warped; a.packed = packed; a.counter = counter;
+  a.img_ring = img_ring; a.feat_ring = feat_ring; a.desire_ring = desire_ring;
+  a.img_out = img_out; a.feat_out = feat_out; a.ctx_tail = ctx_tail;
+  a.frame_units = (int)(frame_bytes / 16);
+  a.img_slots = q.img_slots; a.fs = q.fs;
+  a.feat_len = q.feat_len; a.feat_hist = q.feat_hist; a.desire_len = q.desire_len; a.desire_hist = q.desire_hist;
+  a.n_img = 2 * a.frame_units;
+  a.n_feat = q.feat_hist * q.feat_len;
+  a.n_feat_push = q.feat_len;
+  a.n_des = q.desire_hist * q.desire_len;
+  a.n_des_push = q.desire_len;
+  const long total = (long)a.n_img + a.n_feat + a.n_feat_push + a.n_des + a.n_des_push + 4;
+  hipLaunchKernelGGL(policy_inputs_kernel, dim3(ceil_div(total, 256)), dim3(256), 0, s, a);
+  CK_LAUNCHED("policy_inputs");
+}
+
+void launch_yuv_to_channels(const uint8_t* Y, const uint8_t* U, const uint8_t* V, int H, int W, uint8_t* out,
+                            hipStream_t s) {
+  CK_REQUIRE(Y && U && V && out, "yuv_to_channels: null pointer");
+  CK_REQUIRE(H > 0 && W > 0 && H % 2 == 0 && W % 2 == 0, "yuv_to_channels: H and W must be positive and even");
+  hipLaunchKernelGGL(yuv_to_channels_kernel, dim3(ceil_div((long)(H / 2) * (W / 2), 256)), dim3(256), 0, s, Y, U, V,
+                     H, W, out);
+  CK_LAUNCHED("yuv_to_channels");
+}
+
+void launch_i420_to_channels(const uint8_t* frame, int H, int W, uint8_t* out, hipStream_t s) {
+  CK_REQUIRE(frame && out, "i420_to_channels: null pointer");
+  CK_REQUIRE(H > 0 && W > 0 && H % 4 == 0 && W % 2 == 0, "i420_to_channels: H must be a multiple of 4, W even");
+  hipLaunchKernelGGL(i420_to_channels_kernel, dim3(ceil_div((long)(H / 2) * (W / 2), 256)), dim3(256), 0, s, frame,
+                     H, W, out);
+  CK_LAUNCHED("i420_to_channels");
+}
+
+void launch_img_gather(const void* img, int A, int B, int lanes, int elem_bytes, const int* yx, int n, void* out,
+                       hipStream_t s) {
+  CK_REQUIRE(img && yx && out, "img_gather: null pointer");
+  CK_REQUIRE(A > 0 && B > 0 && (long)A * B < (1L << 31), "img_gather: bad image size");
+  if (n <= 0) return;
+  const int tb = lanes * elem_bytes;
+  CK_REQUIRE((reinterpret_cast<uintptr_t>(img) % tb) == 0 && (reinterpret_cast<uintptr_t>(out) % tb) == 0,
+             "img_gather: image and output must be aligned to the texel size");
+  switch (tb) {
+    case 1: gather_launch<Texel<1, uint8_t>>(img, A, B, yx, n, out, s); break;
+    case 2: gather_launch<Texel<1, uint16_t>>(img, A, B, yx, n, out, s); break;
+    case 4: gather_launch<Texel<1, uint32_t>>(img, A, B, yx, n, out, s); break;
+    case 8: gather_launch<Texel<2, uint32_t>>(img, A, B, yx, n, out, s); break;
+    case 16: gather_launch<Texel<4, uint32_t>>(img, A, B, yx, n, out, s); break;
+    default: throw Error("img_gather: texel size must be 1, 2, 4, 8 or 16 bytes");
+  }
+}
+
+void launch_im2col_u8(const uint8_t* img, int batch, int C, int H, int W, half_t* patches, int Kp, hipStream_t s) {
+  CK_REQUIRE(img && patches && batch > 0, "im2col_u8: bad arguments");
+  CK_REQUIRE(Kp >= 9 * C, "im2col_u8: Kp too small");
+  const int Ho = (H - 1) / 2 + 1, Wo = (W - 1) / 2 + 1;
+  const long per = (long)Ho * Wo * Kp;
+  hipLaunchKernelGGL(im2col_u8_kernel, dim3(ceil_div(per, 256), batch), dim3(256), 0, s, img, C, H, W, patches, Kp,
+                     Ho, Wo);
+  CK_LAUNCHED("im2col_u8");
+}
+
+void launch_im2col_f16(const half_t* act, int batch, int C, int H, int W, half_t* patches, int Kp, hipStream_t s) {
+  CK_REQUIRE(act && patches && batch > 0, "im2col_f16: bad arguments");
+  CK_REQUIRE(C % 4 == 0 && Kp % 4 == 0 && Kp >= 9 * C, "im2col_f16: C and Kp must be multiples of 4, Kp >= 9C");
+  const int Ho = (H - 1) / 2 + 1, Wo = (W - 1) / 2 + 1;
+  const long per = (long)Ho * Wo * (Kp / 4);
+  hipLaunchKernelGGL(im2col_f16_kernel, dim3(ceil_div(per, 256), batch), dim3(256), 0, s, act, C, H, W, patches, Kp,
+                     Ho, Wo);
+  CK_LAUNCHED("im2col_f16");
+}
+
+void launch_tokens(const half_t* stem_out, int n_spatial, int C5, half_t* F, hipStream_t s) {
+  hipLaunchKernelGGL(tokens_kernel, dim3(ceil_div(2L * n_spatial * C5, 256)), dim3(256), 0, s, stem_out, n_spatial,
+                     C5, F);
+  CK_LAUNCHED("tokens");
+}
+
+}  // namespace ck

@@ -1,0 +1,193 @@
+/*
+ * chestnut.h -- C ABI of the MI355X (gfx950) per-frame driving-model engine.
+ *
+ * The reference exposes its hot path as a Python namespace obtained by
+ * exec-ing run_pinned2.py up to '# --- smoke run' (run_pinned2.py:1574,
+ * video_check.py:18-19): run_frame, out_slices, make_warped, queues, PACKED.
+ * Its device work goes through the CUDA driver API via tinygrad's ctypes
+ * bindings.  This header is the native boundary that replaces both: plain
+ * pointers and sizes, no framework types.  A ctypes binding of it (the
+ * package's chestnut/_lib.py) restores the reference's Python surface.
+ *
+ * Conventions
+ *  - Every function returns 0 on success and nonzero on failure; the failure
+ *    message is ck_last_error() (thread-local).  The Python layer raises
+ *    RuntimeError with it, as the reference's `check` does on CUDA status
+ *    codes (run_pinned2.py:1317-1320, 1440).
+ *  - `stream` arguments are hipStream_t passed as void* (NULL = null stream).
+ *  - Device-pointer entry points validate shapes and alignment on the host
+ *    and return an error instead of launching anything out of bounds.
+ *  - An engine handle owns one HIP stream; it is not reentrant (one caller
+ *    thread at a time), like the reference's module globals
+ *    (run_pinned2.py:1424-1431).
+ */
+#ifndef CHESTNUT_H
+#define CHESTNUT_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ck_engine ck_engine;
+
+/* Thread-local message of the last failure ("" if none).
+ * Replaces: RuntimeError raised by `check` (run_pinned2.py:1317-1320). */
+const char* ck_last_error(void);
+
+/* Library version (major, minor). */
+int ck_version(int* major, int* minor);
+
+/* ------------------------------------------------------------------------ */
+/* Engine: model, queues, frame plan, graph                                  */
+/* ------------------------------------------------------------------------ */
+
+/* Build an engine for a model spec (flat JSON, see chestnut/spec.py):
+ * allocates parameters, queue rings, activations, resolves the frame plan.
+ * Replaces: pickle load + reprepare + graph flatten + queue allocation
+ * (run_pinned2.py:1346-1389). */
+int ck_create(const char* spec_json, ck_engine** out);
+int ck_destroy(ck_engine* e);
+
+/* Parameter table (same order as chestnut/spec.py param_table).
+ * dtype: 0 = f32, 1 = f16.  nbytes = logical (unpadded) size.
+ * Replaces: the weights carried inside the pickle (run_pinned2.py:1349). */
+int ck_param_count(ck_engine* e, int* n);
+int ck_param_info(ck_engine* e, int i, char* name, size_t name_len, size_t* nbytes, int* dtype);
+int ck_upload_param(ck_engine* e, const char* name, const void* host, size_t nbytes);
+
+/* Output vector size and the name -> [start, stop) map as JSON, e.g.
+ * {"plan":[0,990],...,"hidden_state":[1673,2185]}.
+ * Replaces: out_slices = meta['output_slices'] (run_pinned2.py:1353-1354). */
+int ck_output_size(ck_engine* e, int* n);
+int ck_output_slices(ck_engine* e, char* buf, size_t len);
+
+/* One policy frame.  warped: uint8 [2][6][img_h][img_w] host array;
+ * packed: f32 [desire 8 | traffic_convention 2 | action_t 2 | prev_feat 512];
+ * out: f32 [ck_output_size].  The first call (graph mode) captures the plan
+ * into a hipGraph; every call is H2D staging + one graph launch + D2H.
+ * Replaces: run_frame(warped_np, packed) (run_pinned2.py:1462-1565). */
+int ck_run_frame(ck_engine* e, const uint8_t* warped, const float* packed, float* out);
+
+/* 1 = replay the plan as one hipGraph launch per frame (default),
+ * 0 = launch the plan kernel by kernel.
+ * Replaces: REPLAY=1 / REPLAY=0 (run_pinned2.py:1391-1403, 1567-1571). */
+int ck_set_graph(ck_engine* e, int on);
+int ck_graph_nodes(ck_engine* e, size_t* n);
+
+/* Zero the queues and the frame counter (fresh input queues).
+ * Replaces: make_input_queues (compile_modeld.py:149-163, run_pinned2.py:1379-1386). */
+int ck_reset(ck_engine* e);
+
+/* Device-resident frame: launch the frame on the engine's own input tensors
+ * ("warped", "packed") without host copies and without synchronising.  The
+ * frame ends by writing its hidden state into packed's prev_feat slot, so
+ * back-to-back launches are the recurrent frame loop of
+ * run_pinned2.py:1576-1587 with the host round trip removed. */
+int ck_frame_launch(ck_engine* e);
+int ck_synchronize(ck_engine* e);
+int ck_stream(ck_engine* e, void** stream);
+
+/* Resolved plan: number of launches and, per launch, its plan name, kernel
+ * family and algorithmic flops / HBM bytes.
+ * Replaces: the recorded _plan list (run_pinned2.py:1466-1475). */
+int ck_plan_size(ck_engine* e, int* n);
+int ck_plan_entry(ck_engine* e, int i, char* name, size_t name_len, char* kernel, size_t kernel_len, double* flops,
+                  double* bytes);
+
+/* Run one eager frame with an event pair around every launch and a
+ * synchronise after each; ms[i] = launch i's time.  n >= plan size.
+ * Replaces: KSYNC=1 (run_pinned2.py:1513-1557). */
+int ck_kernel_times(ck_engine* e, float* ms, int n);
+
+/* Launch plan entries [first, last) eagerly and synchronise.
+ * Replaces: the per-launch bisect of research/xcheck.py:65-124 (XINJECT). */
+int ck_run_range(ck_engine* e, int first, int last);
+
+/* Launch plan entries idx[0..n) in order, `reps` times over, between two HIP
+ * events recorded on the engine's stream; *ms = elapsed time of all
+ * n * reps launches.  Used to time one kernel family live (e.g. every
+ * layer's MLP-up GEMM, so each launch streams its own weights).
+ * Replaces: the per-kernel bench loop of bench_r62.py:25-37. */
+int ck_time_launches(ck_engine* e, const int* idx, int n, int reps, float* ms);
+
+/* Named device tensors (parameters, inputs, queue rings, activations):
+ * device pointer + logical size, and synchronous host copies.
+ * Replaces: KDUMP pre-state dumps (run_pinned2.py:1533-1545) and the
+ * probes' cuMemcpyDtoH captures (r62_probe.py:28-37). */
+int ck_tensor(ck_engine* e, const char* name, void** dptr, size_t* nbytes);
+int ck_read_tensor(ck_engine* e, const char* name, void* host, size_t nbytes);
+int ck_write_tensor(ck_engine* e, const char* name, const void* host, size_t nbytes);
+
+/* ------------------------------------------------------------------------ */
+/* Per-kernel entry points (device pointers) for the probe / bench harness  */
+/* ------------------------------------------------------------------------ */
+
+/* y[r] = act(sum_k W[r*ldw+k] x[k] + bias[r]); W f16, x/y/bias f32; bias may
+ * be NULL; act 0 = none, 1 = gelu(tanh).  K % 8 == 0, K <= 16384, ldw % 8 == 0,
+ * W and x 16-byte aligned.  rows_per_wg 0 = automatic.
+ * Replaces: launch of r_32_32_3_12288_32 (bench_alu.py:13-29; its
+ * warp-split form run_pinned2.py:989-1066). */
+int ck_gemv(const void* W, const float* x, const float* bias, float* y, int rows, int K, int ldw, int act,
+            int rows_per_wg, void* stream);
+
+/* C f32 [M][N] = A f16 [M][K] (lda) * B, B f16 either [K][N] (b_kn = 1, ldb)
+ * or [N][K] (b_kn = 0, ldb); optional bias f32 [N].  K % 64 == 0.
+ * tile: 0 auto, 1 128x128, 2 128x64, 3 64x128, 4 64x64; split_k: 0 auto.
+ * workspace: split_k * M * N floats when split_k > 1 (query with
+ * ck_gemm_workspace, which also resolves auto tile/split).
+ * Replaces: launch of the WMMA GEMM kernels r_6_2 / r_2_24 / r_12_32_4 /
+ * r_48_32_4 (bench_r62.py:13-29, bench_r12.py, bench_r48.py). */
+int ck_gemm_workspace(int M, int N, int K, int b_kn, int* tile, int* split_k, size_t* ws_bytes);
+int ck_gemm(const void* A, const void* B, float* C, const float* bias, int M, int N, int K, long lda, long ldb,
+            long ldc, int b_kn, int tile, int split_k, void* workspace, size_t ws_bytes, void* stream);
+
+/* f16 GEMM with a fused epilogue, as the frame plan uses it.
+ * epi: 1 f16(acc+bias), 2 f16(relu(acc+bias)), 3 f16(gelu(acc+bias)),
+ *      4 C f32 += acc + bias.  B is [N][K]. */
+int ck_gemm_epi(const void* A, const void* B, void* C, const float* bias, int M, int N, int K, long lda, long ldb,
+                long ldc, int epi, int tile, int split_k, void* workspace, size_t ws_bytes, void* stream);
+
+/* n_tiles WMMA uops ((16,16,16), half, 'AMD', 32): per tile u16 fragA[32][8],
+ * fragB[32][8], f32 fragC[32][8] -> f32 fragD[32][8], RDNA4 lane layout.
+ * Replaces: _wm_emit's WMMA lowering (run_pinned2.py:119-266) and the
+ * consumer probe (consumer_probe.py). */
+int ck_wmma_rdna4(const uint16_t* fragA, const uint16_t* fragB, const float* fragC, float* fragD, int n_tiles,
+                  void* stream);
+
+/* One MFMA on row-major operands (variant 0: 16x16x32, A [16][32], B [32][16];
+ * variant 1: 32x32x16, A [32][16], B [16][32]) -> D f32.  Layout KAT for the
+ * operand maps the GEMM and attention kernels use.
+ * Replaces: mma_probe.py's fragment-layout probe (mma_probe.py:10-105). */
+int ck_mfma_kat(int variant, const uint16_t* A, const uint16_t* B, float* D, void* stream);
+
+/* YUV planes uint8 [H][W] each -> uint8 [6][H/2][W/2] = Y00,Y10,Y01,Y11,U,V.
+ * Replaces: rgb_to_channels' packing (video_check.py:27-32). */
+int ck_pack_yuv(const uint8_t* Y, const uint8_t* U, const uint8_t* V, int H, int W, uint8_t* out, void* stream);
+
+/* I420 frame uint8 [H*3/2][W] -> uint8 [6][H/2][W/2].
+ * Replaces: frames_to_tensor (compile_modeld.py:83-92). */
+int ck_frames_to_tensor(const uint8_t* frame, int H, int W, uint8_t* out, void* stream);
+
+/* Zero-border image2d gather: img = A rows x B texels x lanes elements of
+ * elem_bytes; yx = int32 [n][2] (y, x); out [n][lanes].
+ * Replaces: the image branch of _addrflat + masked LOAD
+ * (run_pinned2.py:56-84, 355-374); semantics of research/probe_sampler.py. */
+int ck_img_gather(const void* img, int A, int B, int lanes, int elem_bytes, const int32_t* yx, int n, void* out,
+                  void* stream);
+
+/* Multi-head attention on a packed QK tensor f16 [T][2d] and V^T f16 [d][T]
+ * -> f16 [T][d].  T % 64 == 0, T <= 512, head_dim 64 or 128. */
+int ck_attention(const void* qk, const void* vt, void* out, int T, int n_heads, int head_dim, void* stream);
+
+/* Row LayerNorm of x f32 [rows][d] -> f16 (out_f16 = 1) or f32. */
+int ck_layernorm(const float* x, const float* g, const float* b, void* out, int out_f16, int rows, int d, float eps,
+                 void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CHESTNUT_H */

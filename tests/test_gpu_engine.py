@@ -1,0 +1,221 @@
+"""GPU parity of the frame engine (run_frame and its plan) against the oracle.
+
+Queues and packing are compared bit for bit; network outputs within
+1e-3 relative (max-abs error over a slice / max-abs of that slice), the
+north-star bound for plan outputs."""
+import numpy as np
+import pytest
+
+from chestnut import Engine
+from chestnut import spec as S
+from oracle import model as OM
+from oracle import pack as OP
+
+pytestmark = pytest.mark.gpu
+REL = 1e-3
+
+
+def rel_err(got, ref):
+    return float(np.max(np.abs(got.astype(np.float64) - ref)) / max(np.max(np.abs(ref)), 1e-30))
+
+
+def frame_inputs(rng, spec, n):
+    s = S.get_spec(spec)
+    for _ in range(n):
+        w = rng.integers(0, 256, (2, 6, s['img_h'], s['img_w']), dtype=np.uint8)
+        p = np.zeros(s['desire_len'] + 4 + s['feat_len'], np.float32)
+        p[:8] = (rng.random(8) > 0.7).astype(np.float32)
+        p[8:10] = (1.0, 0.0)
+        p[10:12] = rng.uniform(0, 1, 2)
+        yield w, p
+
+
+@pytest.fixture(scope='module')
+def tiny(gpu):
+    sp = S.get_spec('tiny')
+    w = S.make_weights(sp)
+    eng = Engine(sp, weights=w)
+    yield sp, w, eng
+    eng.close()
+
+
+def test_queue_semantics_bit_exact(tiny):
+    """12+ frames through the device rings == the reference's shift/sample queues."""
+    sp, w, eng = tiny
+    eng.reset()
+    q = OP.PolicyQueues()
+    rng = np.random.default_rng(11)
+    Td = sp['temporal_dim']
+    for f, (warped, packed) in enumerate(frame_inputs(rng, sp, 14)):
+        packed[12:] = rng.standard_normal(512).astype(np.float32)   # host-side prev_feat
+        eng.run_frame(warped, packed)
+        ref = q.step(warped, packed)
+        img = eng.read('img', np.uint8, (2, 12, 128, 256))
+        np.testing.assert_array_equal(img[0], ref['img'], err_msg=f'frame {f} img')
+        np.testing.assert_array_equal(img[1], ref['big_img'], err_msg=f'frame {f} big_img')
+        np.testing.assert_array_equal(eng.read('feat_buf', np.float32, (24, 512)), ref['features_buffer'])
+        tail = eng.read('ctx_in', np.float32)[Td:Td + 204]
+        np.testing.assert_array_equal(tail[:200].reshape(25, 8), ref['desire_pulse'])
+        np.testing.assert_array_equal(tail[200:202], ref['traffic_convention'])
+        np.testing.assert_array_equal(tail[202:204], ref['action_t'])
+
+
+def test_tiny_frames_vs_oracle_with_recurrence(tiny):
+    sp, w, eng = tiny
+    eng.reset()
+    orc = OM.OracleModel(sp, w)
+    rng = np.random.default_rng(12)
+    slices = eng.out_slices
+    pk_dev = None
+    for f, (warped, packed) in enumerate(frame_inputs(rng, sp, 4)):
+        if pk_dev is not None:
+            packed[12:] = pk_dev
+        out = eng.run_frame(warped, packed)
+        ref = orc.run_frame(warped, packed)
+        for name, sl in slices.items():
+            e = rel_err(out[sl], ref[sl])
+            print(f'[tiny] frame {f} {name} rel={e:.2e}', flush=True)
+            assert e <= REL, (f, name, e)
+        pk_dev = out[slices['hidden_state']]
+
+
+def test_stem_and_context_trace(tiny):
+    """Stem output (f16), temporal/context vectors and X0 against the oracle trace."""
+    sp, w, eng = tiny
+    eng.reset()
+    orc = OM.OracleModel(sp, w)
+    rng = np.random.default_rng(13)
+    warped, packed = next(frame_inputs(rng, sp, 1))
+    packed[12:] = rng.standard_normal(512).astype(np.float32) * 0.5
+    eng.run_frame(warped, packed)
+    orc.run_frame(warped, packed)
+    tr = orc.trace
+    for s in range(2):
+        so = eng.read(f'stem.{len(sp["stem"]) - 1}.out', np.float16).reshape(2, 4, 8, -1)[s].astype(np.float64)
+        ref = tr[f'stem{s}']
+        assert rel_err(so, ref) <= REL
+    tok = eng.read('tokens', np.float16, tr['tokens'].shape).astype(np.float64)
+    assert rel_err(tok, tr['tokens']) <= REL
+    Td = sp['temporal_dim']
+    assert rel_err(eng.read('ctx_in', np.float32)[:Td], tr['temporal']) <= 1e-5
+    assert rel_err(eng.read('ctx', np.float32), tr['ctx']) <= 1e-5
+
+
+def test_graph_equals_eager_and_device_loop(tiny):
+    sp, w, eng = tiny
+    rng = np.random.default_rng(14)
+    frames = list(frame_inputs(rng, sp, 3))
+    outs = {}
+    for mode in (True, False):
+        eng.set_graph(mode)
+        eng.reset()
+        res = []
+        hs = None
+        for warped, packed in frames:
+            packed = packed.copy()
+            if hs is not None:
+                packed[12:] = hs
+            o = eng.run_frame(warped, packed)
+            hs = o[eng.out_slices['hidden_state']]
+            res.append(o)
+        outs[mode] = res
+    eng.set_graph(True)
+    for a, b in zip(outs[True], outs[False]):
+        np.testing.assert_array_equal(a, b)
+    assert eng.graph_nodes() >= len(eng.plan())
+    # device-resident loop: same frames, prev_feat fed back on device by the plan itself
+    eng.reset()
+    warped, packed = frames[0]
+    o0 = eng.run_frame(warped, packed)
+    np.testing.assert_array_equal(o0, outs[True][0])
+    eng.write('warped', frames[1][0])
+    p1 = frames[1][1].copy()
+    p1[12:] = eng.read('packed', np.float32)[12:]          # written by the previous frame's tick
+    np.testing.assert_array_equal(p1[12:], outs[True][0][eng.out_slices['hidden_state']])
+    eng.write('packed', p1)
+    eng.frame_launch()
+    eng.synchronize()
+    np.testing.assert_array_equal(eng.read('out', np.float32), outs[True][1])
+
+
+def test_determinism_and_sensitivity(tiny):
+    sp, w, eng = tiny
+    outs = []
+    for val in (40, 40, 220):
+        eng.reset()
+        pk = np.zeros(524, np.float32)
+        for _ in range(3):
+            o = eng.run_frame(eng.make_warped(val), pk)
+            pk[12:] = o[eng.out_slices['hidden_state']]
+        outs.append(o)
+    np.testing.assert_array_equal(outs[0], outs[1])
+    assert np.abs(outs[0] - outs[2]).max() > 1e-4          # bright vs dark A/B differs
+    assert np.all(np.isfinite(outs[2]))
+
+
+def test_kernel_times_cover_plan(tiny):
+    sp, w, eng = tiny
+    plan = eng.kernel_times()
+    assert len(plan) > 20
+    assert all(e['ms'] > 0 for e in plan)
+    names = [e['name'] for e in plan]
+    assert names[0] == 'inputs' and names[-1] == 'tick' and 'blk0.qkv' in names
+
+
+def test_config3_single_block(gpu):
+    """one d=2048, 16x128, T=512, MLP 8192 pre-LN block,
+    x ~ N(0,1); injected into the plan's residual and run alone."""
+    sp = dict(S.get_spec('big_driving_1b'), n_layers=1, name='block')
+    w = S.make_weights(sp)
+    with Engine(sp, weights=w) as eng:
+        rng = np.random.default_rng(42)
+        x = rng.standard_normal((512, 2048)).astype(np.float32)
+        eng.write('x', x)
+        i0, i1 = eng.plan_index('blk0.ln1'), eng.plan_index('blk0.down')
+        eng.run_range(i0, i1 + 1)
+        got = eng.read('x', np.float32, (512, 2048))
+    ref = OM.block_forward(x, w, 0, sp, acc=np.float64)
+    e = rel_err(got, ref)
+    print(f'[block] rel={e:.2e}', flush=True)
+    assert e <= REL
+    # and the block really changed x
+    assert rel_err(x, ref) > 10 * REL
+
+
+def test_39m_frames_vs_oracle(gpu):
+    sp = S.get_spec('driving_39m')
+    w = S.make_weights(sp)
+    orc = OM.OracleModel(sp, w, acc=np.float64)
+    rng = np.random.default_rng(39)
+    with Engine(sp, weights=w) as eng:
+        hs = None
+        for f, (warped, packed) in enumerate(frame_inputs(rng, sp, 3)):
+            if hs is not None:
+                packed[12:] = hs
+            out = eng.run_frame(warped, packed)
+            ref = orc.run_frame(warped, packed)
+            for name, sl in eng.out_slices.items():
+                e = rel_err(out[sl], ref[sl])
+                print(f'[39m] frame {f} {name} rel={e:.2e}', flush=True)
+                assert e <= REL, (f, name, e)
+            hs = out[eng.out_slices['hidden_state']]
+
+
+def test_1b_frames_vs_oracle(gpu):
+    sp = S.get_spec('big_driving_1b')
+    w = S.make_weights(sp)
+    orc = OM.OracleModel(sp, w, acc=np.float32)
+    rng = np.random.default_rng(1000)
+    with Engine(sp, weights=w) as eng:
+        hs = None
+        for f, (warped, packed) in enumerate(frame_inputs(rng, sp, 2)):
+            if hs is not None:
+                packed[12:] = hs
+            out = eng.run_frame(warped, packed)
+            print(f'[1b] frame {f} gpu done', flush=True)
+            ref = orc.run_frame(warped, packed)
+            for name, sl in eng.out_slices.items():
+                e = rel_err(out[sl], ref[sl])
+                print(f'[1b] frame {f} {name} rel={e:.2e}', flush=True)
+                assert e <= REL, (f, name, e)
+            hs = out[eng.out_slices['hidden_state']]
