@@ -337,61 +337,77 @@ void ck_engine::build_plan() {
     g.M = T; g.N = d; g.K = 2 * ns; g.epi = EPI_F32_RESID;
     add_gemm("embed", "gemm_resid", g);
   }
-  // 4. transformer blocks
+  // 4. transformer blocks.  The two residual GEMMs (attention output, MLP
+  // down) split K and leave f32 partials in the workspace; the LayerNorm that
+  // follows each of them adds partials + bias into x before normalising.
+  auto resid_split = [&](int M, int N, int K) {
+    const long tiles = (long)ceil_div(M, 128) * ceil_div(N, 128);
+    int s = 1;
+    while (tiles * s * 2 <= 256 && K % (128 * s * 2) == 0 && K / (s * 2) >= 512) s *= 2;
+    return s;
+  };
+  const int s_o = resid_split(T, d, d), s_dn = resid_split(T, d, F);
+  ck_engine* self = this;
+  const long part_stride = (long)T * d;
+  const float* pend_bias = nullptr;   // bias of the GEMM whose partials the next LN must add
+  int pend_split = 0;
+  auto add_ln = [&](const std::string& name, const float* g, const float* bb, void* out, bool f16) {
+    float* x = f32("x");
+    const float* rb = pend_bias;
+    const int ns = pend_split;
+    const int Tt = T;
+    const float eps = sp.eps;
+    const double bytes = (double)Tt * d * (4 + 4 + (f16 ? 2 : 4)) + (ns ? (double)Tt * d * 4 * ns : 0);
+    add(name, ns ? (f16 ? "add_layernorm_f16" : "add_layernorm_f32") : (f16 ? "layernorm_f16" : "layernorm_f32"), 0,
+        bytes, [=](hipStream_t s) {
+          launch_add_layernorm(x, ns ? self->ws : nullptr, ns, part_stride, rb, g, bb, out, f16, Tt, d, eps, s);
+        });
+    pend_bias = nullptr;
+    pend_split = 0;
+  };
   for (int l = 0; l < sp.n_layers; ++l) {
     const std::string p = "blk." + std::to_string(l) + ".";
     const std::string b = "blk" + std::to_string(l) + ".";
-    const float* x = f32("x");
     half_t* hb = h16("h16");
-    const float* g1 = f32(p + "ln1.g");
-    const float* b1 = f32(p + "ln1.b");
-    const int Tt = T;
-    const float eps = sp.eps;
-    add(b + "ln1", "layernorm_f16", 0, (double)Tt * d * 6, [=](hipStream_t s) {
-      launch_layernorm(x, g1, b1, hb, true, Tt, d, eps, s);
-    });
+    add_ln(b + "ln1", f32(p + "ln1.g"), f32(p + "ln1.b"), hb, true);
     GemmDesc q;
     q.A = hb; q.lda = d; q.B = h16(p + "qkv.w"); q.ldb = d; q.C = ptr("qk"); q.ldc = 2 * d;
     q.bias = f32(p + "qkv.b"); q.M = T; q.N = 3 * d; q.K = d; q.epi = EPI_QKV;
     q.vt = h16("vt"); q.qk_cols = 2 * d; q.vt_ld = T;
+    q.tile = 4; q.split = 1;   // 64x64 tiles, two K-groups: many workgroups for the 3d-wide output
     add_gemm(b + "qkv", "gemm_qkv", q);
     const half_t* qk = h16("qk");
     const half_t* vt = h16("vt");
     half_t* att = h16("att");
-    const int nh = sp.n_heads, hd = sp.head_dim;
+    const int nh = sp.n_heads, hd = sp.head_dim, Tt = T;
     add(b + "attn", "attention", 4.0 * Tt * Tt * d, (double)Tt * d * 2 * 4, [=](hipStream_t s) {
       launch_attention(qk, vt, att, Tt, nh, hd, s);
     });
     GemmDesc o;
-    o.A = att; o.lda = d; o.B = h16(p + "o.w"); o.ldb = d; o.C = ptr("x"); o.ldc = d;
-    o.bias = f32(p + "o.b"); o.M = T; o.N = d; o.K = d; o.epi = EPI_F32_RESID;
-    add_gemm(b + "o", "gemm_resid", o);
-    const float* g2 = f32(p + "ln2.g");
-    const float* b2 = f32(p + "ln2.b");
-    add(b + "ln2", "layernorm_f16", 0, (double)Tt * d * 6, [=](hipStream_t s) {
-      launch_layernorm(x, g2, b2, hb, true, Tt, d, eps, s);
-    });
+    o.A = att; o.lda = d; o.B = h16(p + "o.w"); o.ldb = d;
+    o.M = T; o.N = d; o.K = d; o.epi = EPI_PARTIALS; o.tile = 1; o.split = s_o;
+    add_gemm(b + "o", "gemm_partials", o);
+    pend_bias = f32(p + "o.b");
+    pend_split = s_o;
+    add_ln(b + "ln2", f32(p + "ln2.g"), f32(p + "ln2.b"), hb, true);
     GemmDesc up;
     up.A = hb; up.lda = d; up.B = h16(p + "up.w"); up.ldb = d; up.C = ptr("u"); up.ldc = F;
     up.bias = f32(p + "up.b"); up.M = T; up.N = F; up.K = d; up.epi = EPI_F16_BIAS_GELU;
+    up.tile = 5; up.split = 1;  // 128x128 tiles, one K-group, 5-stage ring
     add_gemm(b + "up", "gemm_gelu", up);
     GemmDesc dn;
-    dn.A = h16("u"); dn.lda = F; dn.B = h16(p + "down.w"); dn.ldb = F; dn.C = ptr("x"); dn.ldc = d;
-    dn.bias = f32(p + "down.b"); dn.M = T; dn.N = d; dn.K = F; dn.epi = EPI_F32_RESID;
-    add_gemm(b + "down", "gemm_resid", dn);
+    dn.A = h16("u"); dn.lda = F; dn.B = h16(p + "down.w"); dn.ldb = F;
+    dn.M = T; dn.N = d; dn.K = F; dn.epi = EPI_PARTIALS; dn.tile = 1; dn.split = s_dn;
+    add_gemm(b + "down", "gemm_partials", dn);
+    pend_bias = f32(p + "down.b");
+    pend_split = s_dn;
   }
-  // 5. final LN + pool, GRU, heads, tick
+  // 5. final LN (adds the last block's MLP partials) + pool, GRU, heads, tick
   {
-    const float* x = f32("x");
     float* xf = f32("xf");
-    const float* gf = f32("lnf.g");
-    const float* bf = f32("lnf.b");
     float* pooled = f32("pooled");
     const int Tt = T;
-    const float eps = sp.eps;
-    add("final.ln", "layernorm_f32", 0, (double)Tt * d * 8, [=](hipStream_t s) {
-      launch_layernorm(x, gf, bf, xf, false, Tt, d, eps, s);
-    });
+    add_ln("final.ln", f32("lnf.g"), f32("lnf.b"), xf, false);
     add("final.pool", "colmean", 0, (double)Tt * d * 4, [=](hipStream_t s) { launch_colmean(xf, pooled, Tt, d, s); });
     const float* hprev = f32("packed") + dl + 4;
     float* gi = f32("gi");

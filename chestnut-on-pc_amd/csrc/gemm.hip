@@ -57,7 +57,7 @@ __device__ __forceinline__ void epi_store(const GemmParams& p, void* C, const fl
   } else {
     if (bias) v += bias[n];
     if (EPI == EPI_F16_BIAS_RELU) v = fmaxf(v, 0.f);
-    if (EPI == EPI_F16_BIAS_GELU) v = gelu_tanh(v);
+    if (EPI == EPI_F16_BIAS_GELU) v = gelu_fast(v);
     if (EPI == EPI_QKV && n >= p.qk_cols) {
       p.vt[(long)(n - p.qk_cols) * p.vt_ld + m] = (half_t)v;
     } else {
@@ -198,7 +198,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(const GemmParams p) {
   }
 
   // ---- epilogue ----
-  if (p.split > 1) {
+  if (p.split > 1 || EPI == EPI_PARTIALS) {
     float* ws = p.ws + ((long)sp * p.batch + bz) * (long)p.M * p.N;
 #pragma unroll
     for (int i = 0; i < FM; ++i)
@@ -246,6 +246,212 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const GemmParams p) 
   epi_store<EPI>(p, C, bias, m, n, v);
 }
 
+// ---------------------------------------------------------------------------
+// NT GEMM with direct global->LDS loads (gfx950 global_load_lds_dwordx4) into
+// an S-stage LDS ring, issued S-1 K-steps ahead of the MFMAs.
+//
+// * No staging registers and no ds_write: each load instruction of a wave
+//   deposits 64 lanes x 16 bytes = 8 tile rows x 128 bytes contiguously.
+// * LDS rows (128 bytes) are stored XOR-swizzled by 16-byte chunk: physical
+//   chunk p of row r holds logical chunk p ^ ((r >> 1) & 7).  The LDS serves
+//   16 lanes x 16 bytes per cycle over 64 banks; two consecutive rows fill the
+//   256-byte bank window, and the swizzle gives the 8 even (odd) rows of any
+//   16 consecutive ones 8 distinct chunk positions, so the MFMA operand reads
+//   are conflict free.  The swizzle is applied through the global addresses
+//   each lane fetches.
+// * One barrier per K-step: each wave waits (vmcnt) only for its own loads of
+//   the step about to be consumed, then the barrier publishes every wave's
+//   loads and retires the previous step's readers, whose stage is refilled.
+//   The barrier is the raw s_barrier: the release fence of __syncthreads
+//   would drain vmcnt to zero on gfx9 and serialise the prefetch.
+// ---------------------------------------------------------------------------
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+template <int N>
+__device__ __forceinline__ void wait_vm_lgkm0() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  // gfx9 s_waitcnt: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt_hi[15:14]
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (0x0 << 8) | (((N >> 4) & 0x3) << 14));
+}
+
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// Issue one K-step's loads of this wave into LDS stage `st` (A rows then B rows).
+template <int NIA, int NIB, int STAGE_A>
+__device__ __forceinline__ void dma_issue(const half_t* const* asrc, const half_t* const* bsrc, half_t* st, int wave,
+                                          int ko) {
+#pragma unroll
+  for (int i = 0; i < NIA; ++i)
+    __builtin_amdgcn_global_load_lds(asrc[i] + ko, (lds_ptr_t)(st + (wave * NIA + i) * 8 * BK), 16, 0, 0);
+#pragma unroll
+  for (int i = 0; i < NIB; ++i)
+    __builtin_amdgcn_global_load_lds(bsrc[i] + ko, (lds_ptr_t)(st + STAGE_A + (wave * NIB + i) * 8 * BK), 16, 0,
+                                     0);
+}
+
+// KG K-groups of 4 waves each (256*KG threads): group g consumes K-steps
+// g, g+KG, g+2KG, ... through its own S/KG stages of the ring, so KG=2 puts
+// 8 waves on a CU for one output tile (twice the loads in flight) without a
+// global split-K reduce; the groups' accumulators are summed through LDS at
+// the end (group 0 + group 1, fixed order).
+template <int BM, int BN, int S, int KG, int EPI>
+__global__ __launch_bounds__(256 * KG) void gemm_dma_kernel(const GemmParams p) {
+  constexpr int STAGE_A = BM * BK, STAGE_B = BN * BK, STAGE = STAGE_A + STAGE_B;   // halves
+  static_assert(S % KG == 0 && S / KG >= 2, "each K-group owns at least two ring stages");
+  constexpr int P = S / KG - 1;   // steps a group keeps in flight while it computes
+  __shared__ __attribute__((aligned(1024))) half_t lds[S * STAGE];
+  constexpr int WM = BM / 2, WN = BN / 2;
+  constexpr int FM = WM / 32, FN = WN / 32;
+  constexpr int NIA = BM / 32, NIB = BN / 32;   // load instructions per wave per step
+  constexpr int NI = NIA + NIB;
+  static_assert(KG == 1 || 4 * FM * FN * 16 * 64 * 4 <= S * STAGE * 2, "LDS too small for the group combine");
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int grp = wave >> 2, w4 = wave & 3;
+  const int wm = w4 >> 1, wn = w4 & 1;
+
+  const int total = p.Mt * p.Nt * p.split * p.batch;
+  int L = blockIdx.x;
+  if ((total & 7) == 0) L = (L & 7) * (total >> 3) + (L >> 3);
+  const int mt = L % p.Mt; L /= p.Mt;
+  const int nt = L % p.Nt; L /= p.Nt;
+  const int sp = L % p.split;
+  const int bz = L / p.split;
+  const int m0 = mt * BM, n0 = nt * BN;
+  const int kbeg = sp * p.kps;
+  const int nkg = p.kps / (BK * KG);   // steps per group (host checks divisibility)
+
+  // per-lane sources: instruction i of wave w4 fills rows (w4*NIA + i)*8 + lane/8;
+  // physical chunk lane%8 <- logical chunk (lane%8) ^ ((row >> 1) & 7)
+  const half_t* asrc[NIA];
+  const half_t* bsrc[NIB];
+#pragma unroll
+  for (int i = 0; i < NIA; ++i) {
+    const int r = (w4 * NIA + i) * 8 + (lane >> 3);
+    const int q = (lane & 7) ^ ((r >> 1) & 7);
+    asrc[i] = p.A + bz * p.sA + (long)min(m0 + r, p.M - 1) * p.lda + kbeg + q * 8;
+  }
+#pragma unroll
+  for (int i = 0; i < NIB; ++i) {
+    const int r = (w4 * NIB + i) * 8 + (lane >> 3);
+    const int q = (lane & 7) ^ ((r >> 1) & 7);
+    bsrc[i] = p.B + bz * p.sB + (long)min(n0 + r, p.N - 1) * p.ldb + kbeg + q * 8;
+  }
+  float16_t acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = float16_t{};
+
+  // group step t is global step KG*t + grp, held in ring stage (KG*t + grp) % S
+#pragma unroll
+  for (int t = 0; t < P; ++t)
+    if (t < nkg) dma_issue<NIA, NIB, STAGE_A>(asrc, bsrc, lds + (KG * t + grp) * STAGE, w4, (KG * t + grp) * BK);
+
+  int aoff[FM], boff[FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i) aoff[i] = (wm * WM + i * 32 + (lane & 31)) * BK;
+#pragma unroll
+  for (int j = 0; j < FN; ++j) boff[j] = (wn * WN + j * 32 + (lane & 31)) * BK;
+  const int rsw = (lane >> 1) & 7;   // ((row >> 1) & 7) of every fragment row this lane reads
+
+  for (int t = 0; t < nkg; ++t) {
+    const int ahead = min(P - 1, nkg - 1 - t);   // this group's later steps already in flight
+    if (P >= 4 && ahead >= 3) wait_vm_lgkm0<3 * NI>();
+    else if (P >= 3 && ahead >= 2) wait_vm_lgkm0<2 * NI>();
+    else if (P >= 2 && ahead >= 1) wait_vm_lgkm0<NI>();
+    else wait_vm_lgkm0<0>();
+    lds_barrier();
+    // refill the stage this group consumed at step t-1 (every wave passed the barrier)
+    if (t + P < nkg)
+      dma_issue<NIA, NIB, STAGE_A>(asrc, bsrc, lds + ((KG * (t + P) + grp) % S) * STAGE, w4, (KG * (t + P) + grp) * BK);
+    const half_t* sa = lds + ((KG * t + grp) % S) * STAGE;
+    const half_t* sb = sa + STAGE_A;
+#pragma unroll
+    for (int kk = 0; kk < BK / 16; ++kk) {
+      const int ch = ((kk * 2 + (lane >> 5)) ^ rsw) * 8;
+      half8_t af[FM], bf[FN];
+#pragma unroll
+      for (int i = 0; i < FM; ++i) af[i] = *reinterpret_cast<const half8_t*>(sa + aoff[i] + ch);
+#pragma unroll
+      for (int j = 0; j < FN; ++j) bf[j] = *reinterpret_cast<const half8_t*>(sb + boff[j] + ch);
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+    }
+  }
+
+  if (KG > 1) {   // group 1 hands its partial tile to group 0 through LDS
+    float* red = reinterpret_cast<float*>(lds);
+    wait_vm_lgkm0<0>();
+    lds_barrier();
+    if (grp == 1) {
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) red[((w4 * FM * FN + i * FN + j) * 16 + e) * 64 + lane] = acc[i][j][e];
+    }
+    wait_vm_lgkm0<0>();
+    lds_barrier();
+    if (grp == 1) return;   // no barrier follows
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[i][j][e] += red[((w4 * FM * FN + i * FN + j) * 16 + e) * 64 + lane];
+  }
+
+  if (p.split > 1 || EPI == EPI_PARTIALS) {
+    float* ws = p.ws + ((long)sp * p.batch + bz) * (long)p.M * p.N;
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int m = m0 + wm * WM + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+          const int n = n0 + wn * WN + j * 32 + (lane & 31);
+          if (m < p.M && n < p.N) ws[(long)m * p.N + n] = acc[i][j][e];
+        }
+    return;
+  }
+  void* C = (EPI == EPI_F32 || EPI == EPI_F32_RESID)
+                ? static_cast<void*>(static_cast<float*>(p.C) + bz * p.sC)
+                : static_cast<void*>(static_cast<half_t*>(p.C) + bz * p.sC);
+  const float* bias = p.bias ? p.bias + bz * p.sBias : nullptr;
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int m = m0 + wm * WM + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+        const int n = n0 + wn * WN + j * 32 + (lane & 31);
+        if (m < p.M && n < p.N) epi_store<EPI>(p, C, bias, m, n, acc[i][j][e]);
+      }
+}
+
+// LDS-DMA kernel configurations: KG = 2 (8 waves) where K allows, else KG = 1.
+template <int BM, int BN, int EPI>
+void launch_dma_tile(const GemmParams& p, bool kg2, hipStream_t s) {
+  const int grid = p.Mt * p.Nt * p.split * p.batch;
+  constexpr int stage_bytes = (BM + BN) * BK * 2;
+  constexpr int S1 = (5 * stage_bytes <= 163840) ? 5 : 4;
+  constexpr int S2 = (BM == 64 && BN == 64) ? 4 : (6 * stage_bytes <= 163840 ? 6 : 4);
+  if (kg2) hipLaunchKernelGGL((gemm_dma_kernel<BM, BN, S2, 2, EPI>), dim3(grid), dim3(512), 0, s, p);
+  else hipLaunchKernelGGL((gemm_dma_kernel<BM, BN, S1, 1, EPI>), dim3(grid), dim3(256), 0, s, p);
+  CK_LAUNCHED("gemm_dma");
+}
+
 template <int BM, int BN, bool BKN, int EPI>
 void launch_tile(const GemmParams& p, hipStream_t s) {
   const int grid = p.Mt * p.Nt * p.split * p.batch;
@@ -253,9 +459,26 @@ void launch_tile(const GemmParams& p, hipStream_t s) {
   CK_LAUNCHED("gemm");
 }
 
+// tile codes 1-4: NT problems on the LDS-DMA kernel; 11-14 (and every [K][N]
+// problem) on the register-staged kernel.
+// tile codes (BM x BN): 1 128x128, 2 128x64, 3 64x128, 4 64x64.
+//   1-4: LDS-DMA kernel with two K-groups (8 waves) when K per split is a
+//        multiple of 128, else one group;  5-8: LDS-DMA, one group;
+//   11-14 (and every [K][N] problem): register-staged kernel.
 template <bool BKN, int EPI>
 void launch_epi(int tile, const GemmParams& p, hipStream_t s) {
-  switch (tile) {
+  const int c = tile % 10;
+  if (!BKN && tile < 10) {
+    const bool kg2 = c <= 4 && p.kps % (2 * BK) == 0;
+    switch (c > 4 ? c - 4 : c) {
+      case 1: launch_dma_tile<128, 128, EPI>(p, kg2, s); break;
+      case 2: launch_dma_tile<128, 64, EPI>(p, kg2, s); break;
+      case 3: launch_dma_tile<64, 128, EPI>(p, kg2, s); break;
+      default: launch_dma_tile<64, 64, EPI>(p, kg2, s); break;
+    }
+    return;
+  }
+  switch (c) {
     case 1: launch_tile<128, 128, BKN, EPI>(p, s); break;
     case 2: launch_tile<128, 64, BKN, EPI>(p, s); break;
     case 3: launch_tile<64, 128, BKN, EPI>(p, s); break;
@@ -270,8 +493,9 @@ void launch_reduce(const GemmParams& p, hipStream_t s) {
   CK_LAUNCHED("splitk_reduce");
 }
 
-int tile_bm(int tile) { return (tile == 1 || tile == 2) ? 128 : 64; }
-int tile_bn(int tile) { return (tile == 1 || tile == 3) ? 128 : 64; }
+int tile_base(int tile) { const int c = tile % 10; return c > 4 ? c - 4 : c; }
+int tile_bm(int tile) { return (tile_base(tile) == 1 || tile_base(tile) == 2) ? 128 : 64; }
+int tile_bn(int tile) { return (tile_base(tile) == 1 || tile_base(tile) == 3) ? 128 : 64; }
 
 }  // namespace
 
@@ -287,8 +511,8 @@ size_t gemm_plan(GemmDesc& d) {
     if (d.b_kn) bn = 128;
     d.tile = bm == 128 ? (bn == 128 ? 1 : 2) : (bn == 128 ? 3 : 4);
   }
-  CK_REQUIRE(d.tile >= 1 && d.tile <= 4, "gemm: unknown tile code");
-  if (d.b_kn) CK_REQUIRE(d.tile == 1 || d.tile == 3, "gemm: [K][N] B needs a 128-wide N tile");
+  CK_REQUIRE((d.tile >= 1 && d.tile <= 8) || (d.tile >= 11 && d.tile <= 14), "gemm: unknown tile code");
+  if (d.b_kn) CK_REQUIRE(d.tile == 11 || d.tile == 13 || d.tile == 1 || d.tile == 3, "gemm: [K][N] B needs a 128-wide N tile");
   const long tiles = (long)ceil_div(d.M, tile_bm(d.tile)) * ceil_div(d.N, tile_bn(d.tile)) * d.batch;
   if (d.split == 0) {
     // split K only while the grid stays within one wave of 256 CUs
@@ -297,12 +521,12 @@ size_t gemm_plan(GemmDesc& d) {
     d.split = s;
   }
   CK_REQUIRE(d.split >= 1 && d.K % (BK * d.split) == 0, "gemm: K must split into multiples of 64");
-  return d.split > 1 ? (size_t)d.split * d.batch * d.M * d.N : 0;
+  return (d.split > 1 || d.epi == EPI_PARTIALS) ? (size_t)d.split * d.batch * d.M * d.N : 0;
 }
 
 void launch_gemm(GemmDesc d, hipStream_t s) {
   const size_t need = gemm_plan(d);
-  CK_REQUIRE(d.A && d.B && d.C, "gemm: null operand");
+  CK_REQUIRE(d.A && d.B && (d.C || d.epi == EPI_PARTIALS), "gemm: null operand");
   CK_REQUIRE(d.lda >= d.K && d.lda % 8 == 0, "gemm: lda must be >= K and a multiple of 8");
   if (d.b_kn) {
     CK_REQUIRE(d.ldb >= d.N && d.ldb % 8 == 0 && d.N % 8 == 0, "gemm: [K][N] B needs N, ldb multiples of 8");
@@ -311,7 +535,8 @@ void launch_gemm(GemmDesc d, hipStream_t s) {
     CK_REQUIRE(d.ldb >= d.K && d.ldb % 8 == 0, "gemm: ldb must be >= K and a multiple of 8");
   }
   // QKV: only the first qk_cols columns are stored row-major in C
-  CK_REQUIRE(d.ldc >= (d.epi == EPI_QKV ? d.qk_cols : d.N), "gemm: ldc must be >= N (>= qk_cols for QKV)");
+  if (d.epi != EPI_PARTIALS)
+    CK_REQUIRE(d.ldc >= (d.epi == EPI_QKV ? d.qk_cols : d.N), "gemm: ldc must be >= N (>= qk_cols for QKV)");
   CK_REQUIRE((reinterpret_cast<uintptr_t>(d.A) & 15) == 0 && (reinterpret_cast<uintptr_t>(d.B) & 15) == 0,
              "gemm: A and B must be 16-byte aligned");
   CK_REQUIRE(d.sA % 8 == 0 && d.sB % 8 == 0, "gemm: batch strides must keep 16-byte alignment");
@@ -338,6 +563,7 @@ void launch_gemm(GemmDesc d, hipStream_t s) {
     case EPI_F16_BIAS_GELU: launch_epi<false, EPI_F16_BIAS_GELU>(d.tile, p, s); if (d.split > 1) launch_reduce<EPI_F16_BIAS_GELU>(p, s); break;
     case EPI_F32_RESID: launch_epi<false, EPI_F32_RESID>(d.tile, p, s); if (d.split > 1) launch_reduce<EPI_F32_RESID>(p, s); break;
     case EPI_QKV: launch_epi<false, EPI_QKV>(d.tile, p, s); if (d.split > 1) launch_reduce<EPI_QKV>(p, s); break;
+    case EPI_PARTIALS: launch_epi<false, EPI_PARTIALS>(d.tile, p, s); break;
     default: throw Error("gemm: unknown epilogue");
   }
 }

@@ -23,6 +23,8 @@ enum Epi {
   EPI_F16_BIAS_GELU = 3,  // C16 = f16(gelu(acc + bias))
   EPI_F32_RESID = 4,      // C32 += acc (+ bias)
   EPI_QKV = 5,            // f16(acc + bias): n < qk_cols -> C16[m][n], else vt[n-qk_cols][m]
+  EPI_PARTIALS = 6,       // raw f32 acc of split s -> ws[s][M][N] (no bias, no reduce); a
+                          // consumer (the residual-add LayerNorm) sums the splits
 };
 
 struct GemmDesc {
@@ -58,6 +60,10 @@ void launch_attention(const half_t* qk, const half_t* vt, half_t* out, int T, in
 // ---- normalisation / small elementwise ---------------------------------------
 void launch_layernorm(const float* x, const float* g, const float* b, void* out, bool out_f16, int rows,
                       int d, float eps, hipStream_t s);
+// x += ((ws[0] + ws[1]) + ... + ws[nsplit-1]) + rbias (the split-K partials of
+// the GEMM that produced x's update; ws[k] at ws + k*split_stride), then LN.
+void launch_add_layernorm(float* x, const float* ws, int nsplit, long split_stride, const float* rbias, const float* g,
+                          const float* b, void* out, bool out_f16, int rows, int d, float eps, hipStream_t s);
 void launch_colmean(const float* x, float* out, int rows, int d, hipStream_t s);
 void launch_gru_gate(const float* gi, const float* gh, const float* h_prev, float* h_out, float* h_out2,
                      int H, hipStream_t s);

@@ -9,20 +9,32 @@ namespace {
 
 // One wave per row; EPL = d / 64 elements per lane, read lane-strided so
 // every load instruction of the wave covers 256 contiguous bytes.
-template <int EPL, bool OUT_F16>
-__global__ __launch_bounds__(256) void layernorm_kernel(const float* __restrict__ x, const float* __restrict__ g,
-                                                        const float* __restrict__ b, void* __restrict__ out, int rows,
-                                                        float eps) {
+// ADD: the row first takes the residual update of the preceding split-K
+// GEMM, x += ((ws[0] + ws[1]) + ... + ws[S-1]) + bias, written back to x.
+template <int EPL, bool OUT_F16, bool ADD>
+__global__ __launch_bounds__(256) void layernorm_kernel(float* __restrict__ x, const float* __restrict__ ws, int nsplit,
+                                                        long split_stride, const float* __restrict__ rbias,
+                                                        const float* __restrict__ g, const float* __restrict__ b,
+                                                        void* __restrict__ out, int rows, float eps) {
   constexpr int D = EPL * 64;
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (row >= rows) return;   // whole wave leaves together; no barriers below
-  const float* xr = x + (long)row * D;
+  float* xr = x + (long)row * D;
   float v[EPL];
   float s = 0.f;
 #pragma unroll
   for (int i = 0; i < EPL; ++i) {
-    v[i] = xr[lane + 64 * i];
+    const int c = lane + 64 * i;
+    v[i] = xr[c];
+    if (ADD) {
+      const float* w = ws + (long)row * D + c;
+      float a = w[0];
+      for (int k = 1; k < nsplit; ++k) a += w[k * split_stride];
+      if (rbias) a += rbias[c];
+      v[i] = v[i] + a;
+      xr[c] = v[i];
+    }
     s += v[i];
   }
   const float mean = wave_sum(s) / (float)D;
@@ -43,23 +55,113 @@ __global__ __launch_bounds__(256) void layernorm_kernel(const float* __restrict_
   }
 }
 
+// Wide rows (d >= 512): one 256-thread workgroup per row, EPT = d/256
+// elements per thread (coalesced: element tid + 256*i), so a row's x and
+// split-K partial loads are all independent and in flight together.  Row
+// sums: DPP wave sums, then the 4 wave sums combined through LDS in order.
+template <int EPT, bool OUT_F16, bool ADD>
+__global__ __launch_bounds__(256) void layernorm_row_kernel(float* __restrict__ x, const float* __restrict__ ws,
+                                                            int nsplit, long split_stride,
+                                                            const float* __restrict__ rbias,
+                                                            const float* __restrict__ g, const float* __restrict__ b,
+                                                            void* __restrict__ out, float eps) {
+  constexpr int D = EPT * 256;
+  __shared__ float red[2][4];
+  const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  float* xr = x + (long)row * D;
+  float v[EPT];
+#pragma unroll
+  for (int i = 0; i < EPT; ++i) v[i] = xr[tid + 256 * i];
+  if (ADD) {
+    float a[EPT];
+    const float* w = ws + (long)row * D + tid;
+#pragma unroll
+    for (int i = 0; i < EPT; ++i) a[i] = w[256 * i];
+    for (int k = 1; k < nsplit; ++k) {
+#pragma unroll
+      for (int i = 0; i < EPT; ++i) a[i] += w[k * split_stride + 256 * i];
+    }
+#pragma unroll
+    for (int i = 0; i < EPT; ++i) {
+      if (rbias) a[i] += rbias[tid + 256 * i];
+      v[i] = v[i] + a[i];
+      xr[tid + 256 * i] = v[i];
+    }
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < EPT; ++i) s += v[i];
+  s = wave_sum(s);
+  if (lane == 0) red[0][wave] = s;
+  __syncthreads();
+  const float mean = (((red[0][0] + red[0][1]) + red[0][2]) + red[0][3]) / (float)D;
+  float q = 0.f;
+#pragma unroll
+  for (int i = 0; i < EPT; ++i) {
+    const float c = v[i] - mean;
+    q = fmaf(c, c, q);
+  }
+  q = wave_sum(q);
+  if (lane == 0) red[1][wave] = q;
+  __syncthreads();
+  const float var = (((red[1][0] + red[1][1]) + red[1][2]) + red[1][3]) / (float)D;
+  const float rstd = 1.0f / sqrtf(var + eps);
+#pragma unroll
+  for (int i = 0; i < EPT; ++i) {
+    const int c = tid + 256 * i;
+    const float y = (v[i] - mean) * rstd * g[c] + b[c];
+    if (OUT_F16) static_cast<half_t*>(out)[(long)row * D + c] = (half_t)y;
+    else static_cast<float*>(out)[(long)row * D + c] = y;
+  }
+}
+
+template <int EPT>
+void ln_row_launch(float* x, const float* ws, int nsplit, long sstride, const float* rbias, const float* g,
+                   const float* b, void* out, bool f16, int rows, float eps, hipStream_t s) {
+  dim3 grid(rows);
+  if (ws) {
+    if (f16) hipLaunchKernelGGL((layernorm_row_kernel<EPT, true, true>), grid, dim3(256), 0, s, x, ws, nsplit, sstride, rbias, g, b, out, eps);
+    else hipLaunchKernelGGL((layernorm_row_kernel<EPT, false, true>), grid, dim3(256), 0, s, x, ws, nsplit, sstride, rbias, g, b, out, eps);
+  } else {
+    if (f16) hipLaunchKernelGGL((layernorm_row_kernel<EPT, true, false>), grid, dim3(256), 0, s, x, ws, nsplit, sstride, rbias, g, b, out, eps);
+    else hipLaunchKernelGGL((layernorm_row_kernel<EPT, false, false>), grid, dim3(256), 0, s, x, ws, nsplit, sstride, rbias, g, b, out, eps);
+  }
+  CK_LAUNCHED("layernorm_row");
+}
+
 template <int EPL>
-void ln_launch(const float* x, const float* g, const float* b, void* out, bool f16, int rows, float eps,
-               hipStream_t s) {
+void ln_launch(float* x, const float* ws, int nsplit, long sstride, const float* rbias, const float* g, const float* b,
+               void* out, bool f16, int rows, float eps, hipStream_t s) {
   dim3 grid((rows + 3) / 4);
-  if (f16) hipLaunchKernelGGL((layernorm_kernel<EPL, true>), grid, dim3(256), 0, s, x, g, b, out, rows, eps);
-  else hipLaunchKernelGGL((layernorm_kernel<EPL, false>), grid, dim3(256), 0, s, x, g, b, out, rows, eps);
+  if (ws) {
+    if (f16) hipLaunchKernelGGL((layernorm_kernel<EPL, true, true>), grid, dim3(256), 0, s, x, ws, nsplit, sstride, rbias, g, b, out, rows, eps);
+    else hipLaunchKernelGGL((layernorm_kernel<EPL, false, true>), grid, dim3(256), 0, s, x, ws, nsplit, sstride, rbias, g, b, out, rows, eps);
+  } else {
+    if (f16) hipLaunchKernelGGL((layernorm_kernel<EPL, true, false>), grid, dim3(256), 0, s, x, ws, nsplit, sstride, rbias, g, b, out, rows, eps);
+    else hipLaunchKernelGGL((layernorm_kernel<EPL, false, false>), grid, dim3(256), 0, s, x, ws, nsplit, sstride, rbias, g, b, out, rows, eps);
+  }
   CK_LAUNCHED("layernorm");
 }
 
-// out[n] = (1/rows) * sum_t x[t][n], summed in row order (deterministic).
-__global__ __launch_bounds__(256) void colmean_kernel(const float* __restrict__ x, float* __restrict__ out, int rows,
+// out[n] = (1/rows) * sum_t x[t][n].  A workgroup owns 64 columns; its 8
+// waves sum interleaved row subsets (wave w: rows w, w+8, ...), and the 8
+// partial sums are combined in wave order through LDS (deterministic).
+__global__ __launch_bounds__(512) void colmean_kernel(const float* __restrict__ x, float* __restrict__ out, int rows,
                                                       int d) {
-  const int n = blockIdx.x * 256 + threadIdx.x;
-  if (n >= d) return;
+  __shared__ float part[8][64];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int n = blockIdx.x * 64 + lane;
   float s = 0.f;
-  for (int t = 0; t < rows; ++t) s += x[(long)t * d + n];
-  out[n] = s / (float)rows;
+  if (n < d)
+    for (int t = w; t < rows; t += 8) s += x[(long)t * d + n];
+  part[w][lane] = s;
+  __syncthreads();
+  if (w == 0 && n < d) {
+    float a = part[0][lane];
+#pragma unroll
+    for (int k = 1; k < 8; ++k) a += part[k][lane];
+    out[n] = a / (float)rows;
+  }
 }
 
 // GRU update (gate order r, z, n as rows [0,H), [H,2H), [2H,3H)):
@@ -107,20 +209,26 @@ __global__ __launch_bounds__(256) void fill_u32_kernel(unsigned* p, unsigned v, 
 
 void launch_layernorm(const float* x, const float* g, const float* b, void* out, bool out_f16, int rows, int d,
                       float eps, hipStream_t s) {
+  launch_add_layernorm(const_cast<float*>(x), nullptr, 0, 0, nullptr, g, b, out, out_f16, rows, d, eps, s);
+}
+
+void launch_add_layernorm(float* x, const float* ws, int nsplit, long split_stride, const float* rbias, const float* g,
+                          const float* b, void* out, bool out_f16, int rows, int d, float eps, hipStream_t s) {
   CK_REQUIRE(x && g && b && out && rows > 0, "layernorm: bad arguments");
+  CK_REQUIRE(!ws || nsplit >= 1, "layernorm: residual partials need nsplit >= 1");
   switch (d) {
-    case 128: ln_launch<2>(x, g, b, out, out_f16, rows, eps, s); break;
-    case 256: ln_launch<4>(x, g, b, out, out_f16, rows, eps, s); break;
-    case 512: ln_launch<8>(x, g, b, out, out_f16, rows, eps, s); break;
-    case 1024: ln_launch<16>(x, g, b, out, out_f16, rows, eps, s); break;
-    case 2048: ln_launch<32>(x, g, b, out, out_f16, rows, eps, s); break;
+    case 128: ln_launch<2>(x, ws, nsplit, split_stride, rbias, g, b, out, out_f16, rows, eps, s); break;
+    case 256: ln_launch<4>(x, ws, nsplit, split_stride, rbias, g, b, out, out_f16, rows, eps, s); break;
+    case 512: ln_row_launch<2>(x, ws, nsplit, split_stride, rbias, g, b, out, out_f16, rows, eps, s); break;
+    case 1024: ln_row_launch<4>(x, ws, nsplit, split_stride, rbias, g, b, out, out_f16, rows, eps, s); break;
+    case 2048: ln_row_launch<8>(x, ws, nsplit, split_stride, rbias, g, b, out, out_f16, rows, eps, s); break;
     default: throw Error("layernorm: d must be one of 128, 256, 512, 1024, 2048");
   }
 }
 
 void launch_colmean(const float* x, float* out, int rows, int d, hipStream_t s) {
   CK_REQUIRE(x && out && rows > 0 && d > 0, "colmean: bad arguments");
-  hipLaunchKernelGGL(colmean_kernel, dim3(ceil_div(d, 256)), dim3(256), 0, s, x, out, rows, d);
+  hipLaunchKernelGGL(colmean_kernel, dim3(ceil_div(d, 64)), dim3(512), 0, s, x, out, rows, d);
   CK_LAUNCHED("colmean");
 }
 

@@ -171,7 +171,9 @@ def test_config3_single_block(gpu):
         rng = np.random.default_rng(42)
         x = rng.standard_normal((512, 2048)).astype(np.float32)
         eng.write('x', x)
-        i0, i1 = eng.plan_index('blk0.ln1'), eng.plan_index('blk0.down')
+        # the block's MLP-down partials reach x in the LayerNorm that follows
+        # the block (final.ln for a one-block spec), so run through it
+        i0, i1 = eng.plan_index('blk0.ln1'), eng.plan_index('final.ln')
         eng.run_range(i0, i1 + 1)
         got = eng.read('x', np.float32, (512, 2048))
     ref = OM.block_forward(x, w, 0, sp, acc=np.float64)
