@@ -371,19 +371,32 @@ __global__ __launch_bounds__(256 * KG) void gemm_dma_kernel(const GemmParams p) 
       dma_issue<NIA, NIB, STAGE_A>(asrc, bsrc, lds + ((KG * (t + P) + grp) % S) * STAGE, w4, (KG * (t + P) + grp) * BK);
     const half_t* sa = lds + ((KG * t + grp) % S) * STAGE;
     const half_t* sb = sa + STAGE_A;
-#pragma unroll
-    for (int kk = 0; kk < BK / 16; ++kk) {
+    // Two-deep software pipeline over the step's k-slices, each slice's
+    // fragments in registers of their own: the LDS reads of slice kk+2 are
+    // issued behind the MFMAs of slice kk, so reads overlap matrix work and
+    // never wait for the matrix core to release a reused source register
+    // (at most 2 slices = 8 reads outstanding, within lgkmcnt's range).
+    constexpr int KS = BK / 16;
+    half8_t af[KS][FM], bf[KS][FN];
+    auto read_slice = [&](int kk) {
       const int ch = ((kk * 2 + (lane >> 5)) ^ rsw) * 8;
-      half8_t af[FM], bf[FN];
 #pragma unroll
-      for (int i = 0; i < FM; ++i) af[i] = *reinterpret_cast<const half8_t*>(sa + aoff[i] + ch);
+      for (int i = 0; i < FM; ++i) af[kk][i] = *reinterpret_cast<const half8_t*>(sa + aoff[i] + ch);
 #pragma unroll
-      for (int j = 0; j < FN; ++j) bf[j] = *reinterpret_cast<const half8_t*>(sb + boff[j] + ch);
+      for (int j = 0; j < FN; ++j) bf[kk][j] = *reinterpret_cast<const half8_t*>(sb + boff[j] + ch);
+    };
+    read_slice(0);
+    read_slice(1);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int kk = 0; kk < KS; ++kk) {
 #pragma unroll
       for (int i = 0; i < FM; ++i)
 #pragma unroll
         for (int j = 0; j < FN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[kk][i], bf[kk][j], acc[i][j], 0, 0, 0);
+      if (kk + 2 < KS) read_slice(kk + 2);
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
 
