@@ -4,14 +4,23 @@
 // (NOTES.md:84-104); this is the gfx950 form of the same f16-input,
 // f32-accumulate products with an f32 softmax between them.
 //
-// One workgroup = 16 query rows of one head, 4 waves:
-//   1. S = q k^T * scale: each wave takes T/4 keys in 16-key blocks,
-//      v_mfma_f32_16x16x32_f16 with q fragments held in registers and k read
-//      straight from the packed QK tensor (16 bytes per lane); S -> LDS (f32).
-//   2. softmax per row in f32 (max, exp, sum via DPP wave reductions), the
-//      normalised probabilities rounded to f16 into LDS.
-//   3. O = P v: v arrives transposed (V^T [d][T], written by the QKV GEMM
-//      epilogue) so each lane's 8 consecutive keys are one 16-byte load.
+// One workgroup = 32 queries of one head, 4 waves (T=512, 16 heads: 256
+// workgroups, one per CU).  Every K and V element a workgroup needs is read
+// by exactly one of its waves:
+//   1. wave w computes S^T = K Q^T * scale for keys [w*T/4, (w+1)*T/4) and all
+//      32 queries with v_mfma_f32_16x16x32_f16 (A = 16 keys x 32 head dims of
+//      K, B = Q^T); the S^T tile stays in registers (T/8 floats per lane);
+//   2. softmax per query: lane-local max / sum over its keys, xor-16/xor-32
+//      lane exchanges, then the four waves' partials through a 1 KB LDS table
+//      in fixed wave order (deterministic); P = e^(s-max) / sum rounded to f16
+//      into LDS as P[query][key] (the D layout gives each lane four
+//      consecutive keys of one query: one 8-byte LDS write);
+//   3. wave w computes O[:, w*hd/4 .. +hd/4) = P V over all T keys: A = P from
+//      LDS (rows padded to T+8 halves: the 16 rows a 16-lane group reads fall
+//      in distinct banks), B = V^T [d][T] (written transposed by the QKV GEMM
+//      epilogue) so a lane's 8 consecutive keys are one 16-byte load.
+// Workgroups are regrouped by XCD (consecutive ids land on different XCDs):
+// each XCD's L2 then serves the K/V of T*hd*2*2 bytes for 2 heads.
 // MFMA 16x16x32 layout (lane l): A row l%16, k = 8*(l/16)..+7; B column
 // l%16, same k; D element i of lane l is row 4*(l/16)+i, column l%16.
 #include "common.h"
@@ -21,94 +30,204 @@ namespace ck {
 namespace {
 
 constexpr int ATT_TMAX = 512;
-constexpr int ATT_LS = ATT_TMAX + 4;
-constexpr int ATT_LP = ATT_TMAX + 8;
+constexpr int ATT_QB = 32;   // queries per workgroup
 
-template <int HD>
-__global__ __launch_bounds__(256) void attention_kernel(const half_t* __restrict__ qk, const half_t* __restrict__ vt,
-                                                        half_t* __restrict__ out, int T, int d, float scale) {
-  __shared__ float S[16][ATT_LS];
-  __shared__ __attribute__((aligned(16))) half_t P[16][ATT_LP];
-  const int h = blockIdx.y, q0 = blockIdx.x * 16;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+__device__ __forceinline__ float xor_max(float v) {
+  v = fmaxf(v, __shfl_xor(v, 16));
+  return fmaxf(v, __shfl_xor(v, 32));
+}
+__device__ __forceinline__ float xor_sum(float v) {
+  v += __shfl_xor(v, 16);
+  return v + __shfl_xor(v, 32);
+}
+
+// NKT = T / 64; WAVES = 8 (hd 128, T % 128 == 0) or 4.  Every load a wave
+// makes (its Q fragments, its T/WAVES keys, its hd/WAVES columns of V^T) is
+// issued at entry, before any MFMA: the K/V working set of a workgroup
+// (T*hd*2*2 bytes) is then in flight at once instead of a few loads per
+// wave, which is what bounds a one-workgroup-per-CU kernel on data that
+// comes from the Infinity Cache.
+// FRAG: qk / vt hold the operands in MFMA fragment order (written by the
+// QKV GEMM's fragment epilogue): every fragment load of a wave is one
+// contiguous KB.  Otherwise the row layouts: qk [T][2d], vt [d][T].
+template <int HD, int NKT, int WAVES, bool FRAG>
+__global__ __launch_bounds__(64 * WAVES) void attention_kernel(const half_t* __restrict__ qk,
+                                                               const half_t* __restrict__ vt,
+                                                               half_t* __restrict__ out, int n_heads, float scale) {
+  constexpr int T = 64 * NKT;
+  constexpr int KS = HD / 32;        // k-steps of the q.k products
+  constexpr int KPW = T / WAVES;     // keys per wave in phase 1
+  constexpr int KT = KPW / 16;       // 16-key tiles per wave
+  constexpr int CW = HD / WAVES;     // output columns per wave in phase 3
+  constexpr int CT = CW / 16;        // 16-wide output tiles per wave
+  constexpr int NT = T / 32;         // 32-key steps of phase 3
+  constexpr int LP = T + 8;          // P row pitch (halves)
+  static_assert(KPW % 16 == 0 && CW % 16 == 0, "wave split must keep whole MFMA tiles");
+  __shared__ __attribute__((aligned(16))) half_t P[ATT_QB][LP];
+  __shared__ float red[2][WAVES][ATT_QB];
+
+  const int d = n_heads * HD;
+  const int nqb = T / ATT_QB;
+  const int total = nqb * n_heads;
+  int L = blockIdx.x;
+  if ((total & 7) == 0) L = (L & 7) * (total >> 3) + (L >> 3);
+  const int h = L / nqb, q0 = (L % nqb) * ATT_QB;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r16 = lane & 15, g = lane >> 4;
   const long ldq = 2L * d;
+  const int kw0 = wave * KPW;
 
-  constexpr int KS = HD / 32;
-  half8_t qf[KS];
-  const half_t* qrow = qk + (long)(q0 + r16) * ldq + h * HD + g * 8;
+  // ---- all loads up front ----
+  half8_t qf[2][KS], kf[KT][KS], vb[NT][CT];
 #pragma unroll
-  for (int ks = 0; ks < KS; ++ks) qf[ks] = *reinterpret_cast<const half8_t*>(qrow + ks * 32);
-
-  const int kpw = T / 4;
-  for (int kb = wave * kpw; kb < (wave + 1) * kpw; kb += 16) {
-    const half_t* krow = qk + (long)(kb + r16) * ldq + d + h * HD + g * 8;
-    float4_t acc = {0.f, 0.f, 0.f, 0.f};
+  for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks)
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(qf[ks], *reinterpret_cast<const half8_t*>(krow + ks * 32), acc, 0,
-                                                  0, 0);
+      kf[kt][ks] = *reinterpret_cast<const half8_t*>(
+          FRAG ? qk + ((((long)(n_heads + h) * (T / 16) + kw0 / 16 + kt) * KS + ks) * 64 + lane) * 8
+               : qk + (long)(kw0 + kt * 16 + r16) * ldq + d + h * HD + ks * 32 + g * 8);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) S[4 * g + i][kb + r16] = acc[i] * scale;
+  for (int qt = 0; qt < 2; ++qt)
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+      qf[qt][ks] = *reinterpret_cast<const half8_t*>(
+          FRAG ? qk + ((((long)h * (T / 16) + q0 / 16 + qt) * KS + ks) * 64 + lane) * 8
+               : qk + (long)(q0 + qt * 16 + r16) * ldq + h * HD + ks * 32 + g * 8);
+  const half_t* vrow = vt + (long)(h * HD + wave * CW + r16) * T + g * 8;
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct)
+      vb[t][ct] = *reinterpret_cast<const half8_t*>(
+          FRAG ? vt + ((((long)h * (HD / 16) + wave * CT + ct) * NT + t) * 64 + lane) * 8
+               : vrow + (long)ct * 16 * T + t * 32);
+
+  // ---- phase 1: S^T = K Q^T for this wave's keys ----
+  float4_t s[KT][2];
+#pragma unroll
+  for (int kt = 0; kt < KT; ++kt)
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) {
+      float4_t a = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) a = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[kt][ks], qf[qt][ks], a, 0, 0, 0);
+      s[kt][qt] = a * scale;
+    }
+
+  // ---- phase 2: softmax per query (column r16 of q-tile qt) ----
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt) {
+    float m = -INFINITY;
+#pragma unroll
+    for (int kt = 0; kt < KT; ++kt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) m = fmaxf(m, s[kt][qt][i]);
+    m = xor_max(m);
+    if (g == 0) red[0][wave][qt * 16 + r16] = m;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt) {
+    const int q = qt * 16 + r16;
+    float mx = red[0][0][q];
+#pragma unroll
+    for (int w = 1; w < WAVES; ++w) mx = fmaxf(mx, red[0][w][q]);
+    float acc = 0.f;
+#pragma unroll
+    for (int kt = 0; kt < KT; ++kt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float e = expf(s[kt][qt][i] - mx);
+        s[kt][qt][i] = e;
+        acc += e;
+      }
+    acc = xor_sum(acc);
+    if (g == 0) red[1][wave][q] = acc;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt) {
+    const int q = qt * 16 + r16;
+    float sum = red[1][0][q];
+#pragma unroll
+    for (int w = 1; w < WAVES; ++w) sum += red[1][w][q];
+#pragma unroll
+    for (int kt = 0; kt < KT; ++kt) {
+      half4_t pv;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) pv[i] = (half_t)(s[kt][qt][i] / sum);
+      *reinterpret_cast<half4_t*>(&P[q][kw0 + kt * 16 + 4 * g]) = pv;
+    }
   }
   __syncthreads();
 
-  constexpr int NPL = ATT_TMAX / 64;
-  for (int rr = 0; rr < 4; ++rr) {
-    const int r = wave * 4 + rr;
-    float v[NPL];
-    float mx = -INFINITY;
+  // ---- phase 3: O[:, wave's columns] = P V ----
+  float4_t o[2][CT];
 #pragma unroll
-    for (int i = 0; i < NPL; ++i) {
-      const int c = lane + 64 * i;
-      v[i] = c < T ? S[r][c] : -INFINITY;
-      mx = fmaxf(mx, v[i]);
-    }
-    mx = wave_max(mx);
-    float sum = 0.f;
+  for (int qt = 0; qt < 2; ++qt)
 #pragma unroll
-    for (int i = 0; i < NPL; ++i) {
-      const int c = lane + 64 * i;
-      v[i] = c < T ? expf(v[i] - mx) : 0.f;
-      sum += v[i];
-    }
-    sum = wave_sum(sum);
+    for (int ct = 0; ct < CT; ++ct) o[qt][ct] = float4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int i = 0; i < NPL; ++i) {
-      const int c = lane + 64 * i;
-      if (c < T) P[r][c] = (half_t)(v[i] / sum);
-    }
+  for (int t = 0; t < NT; ++t) {
+    half8_t pa[2];
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) pa[qt] = *reinterpret_cast<const half8_t*>(&P[qt * 16 + r16][t * 32 + g * 8]);
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt)
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct)
+        o[qt][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[qt], vb[t][ct], o[qt][ct], 0, 0, 0);
   }
-  __syncthreads();
-
-  for (int cb = wave; cb < HD / 16; cb += 4) {
-    float4_t acc = {0.f, 0.f, 0.f, 0.f};
-    const half_t* vrow = vt + (long)(h * HD + cb * 16 + r16) * T + g * 8;
-    for (int k = 0; k < T; k += 32) {
-      const half8_t pa = *reinterpret_cast<const half8_t*>(&P[r16][k + g * 8]);
-      const half8_t vb = *reinterpret_cast<const half8_t*>(vrow + k);
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, vb, acc, 0, 0, 0);
-    }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) out[(long)(q0 + 4 * g + i) * d + h * HD + cb * 16 + r16] = (half_t)acc[i];
+  for (int qt = 0; qt < 2; ++qt)
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        out[(long)(q0 + qt * 16 + 4 * g + i) * d + h * HD + wave * CW + ct * 16 + r16] = (half_t)o[qt][ct][i];
+}
+
+template <int HD, int NKT, bool FRAG>
+void launch_t(int n_heads, const half_t* qk, const half_t* vt, half_t* out, float scale, hipStream_t s) {
+  const dim3 grid((64 * NKT / ATT_QB) * n_heads);
+  if constexpr (HD == 128 && NKT % 2 == 0)
+    hipLaunchKernelGGL((attention_kernel<HD, NKT, 8, FRAG>), grid, dim3(512), 0, s, qk, vt, out, n_heads, scale);
+  else
+    hipLaunchKernelGGL((attention_kernel<HD, NKT, 4, FRAG>), grid, dim3(256), 0, s, qk, vt, out, n_heads, scale);
+}
+
+template <int HD, bool FRAG>
+void launch_hd(int T, int n_heads, const half_t* qk, const half_t* vt, half_t* out, float scale, hipStream_t s) {
+  switch (T / 64) {
+    case 1: launch_t<HD, 1, FRAG>(n_heads, qk, vt, out, scale, s); break;
+    case 2: launch_t<HD, 2, FRAG>(n_heads, qk, vt, out, scale, s); break;
+    case 3: launch_t<HD, 3, FRAG>(n_heads, qk, vt, out, scale, s); break;
+    case 4: launch_t<HD, 4, FRAG>(n_heads, qk, vt, out, scale, s); break;
+    case 5: launch_t<HD, 5, FRAG>(n_heads, qk, vt, out, scale, s); break;
+    case 6: launch_t<HD, 6, FRAG>(n_heads, qk, vt, out, scale, s); break;
+    case 7: launch_t<HD, 7, FRAG>(n_heads, qk, vt, out, scale, s); break;
+    default: launch_t<HD, 8, FRAG>(n_heads, qk, vt, out, scale, s); break;
   }
 }
 
 }  // namespace
 
-void launch_attention(const half_t* qk, const half_t* vt, half_t* out, int T, int n_heads, int head_dim,
+void launch_attention(const half_t* qk, const half_t* vt, half_t* out, int T, int n_heads, int head_dim, bool frag,
                       hipStream_t s) {
   CK_REQUIRE(qk && vt && out, "attention: null pointer");
   CK_REQUIRE(T > 0 && T % 64 == 0 && T <= ATT_TMAX, "attention: T must be a multiple of 64 and <= 512");
   CK_REQUIRE(head_dim == 64 || head_dim == 128, "attention: head_dim must be 64 or 128");
   CK_REQUIRE(n_heads > 0, "attention: n_heads must be positive");
-  const int d = n_heads * head_dim;
+  CK_REQUIRE((reinterpret_cast<uintptr_t>(qk) & 15) == 0 && (reinterpret_cast<uintptr_t>(vt) & 15) == 0,
+             "attention: qk and vt must be 16-byte aligned");
   const float scale = 1.0f / sqrtf((float)head_dim);
-  dim3 grid(T / 16, n_heads);
-  if (head_dim == 64)
-    hipLaunchKernelGGL(attention_kernel<64>, grid, dim3(256), 0, s, qk, vt, out, T, d, scale);
-  else
-    hipLaunchKernelGGL(attention_kernel<128>, grid, dim3(256), 0, s, qk, vt, out, T, d, scale);
+  if (frag) {
+    if (head_dim == 64) launch_hd<64, true>(T, n_heads, qk, vt, out, scale, s);
+    else launch_hd<128, true>(T, n_heads, qk, vt, out, scale, s);
+  } else {
+    if (head_dim == 64) launch_hd<64, false>(T, n_heads, qk, vt, out, scale, s);
+    else launch_hd<128, false>(T, n_heads, qk, vt, out, scale, s);
+  }
   CK_LAUNCHED("attention");
 }
 

@@ -333,7 +333,7 @@ int ck_img_gather(const void* img, int A, int B, int lanes, int elem_bytes, cons
 int ck_attention(const void* qk, const void* vt, void* out, int T, int n_heads, int head_dim, void* stream) {
   CK_API_BEGIN
   launch_attention(static_cast<const half_t*>(qk), static_cast<const half_t*>(vt), static_cast<half_t*>(out), T,
-                   n_heads, head_dim, as_stream(stream));
+                   n_heads, head_dim, false, as_stream(stream));
   CK_API_END
 }
 

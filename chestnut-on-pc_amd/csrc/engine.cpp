@@ -372,16 +372,16 @@ void ck_engine::build_plan() {
     add_ln(b + "ln1", f32(p + "ln1.g"), f32(p + "ln1.b"), hb, true);
     GemmDesc q;
     q.A = hb; q.lda = d; q.B = h16(p + "qkv.w"); q.ldb = d; q.C = ptr("qk"); q.ldc = 2 * d;
-    q.bias = f32(p + "qkv.b"); q.M = T; q.N = 3 * d; q.K = d; q.epi = EPI_QKV;
-    q.vt = h16("vt"); q.qk_cols = 2 * d; q.vt_ld = T;
-    q.tile = 4; q.split = 1;   // 64x64 tiles, two K-groups: many workgroups for the 3d-wide output
+    q.bias = f32(p + "qkv.b"); q.M = T; q.N = 3 * d; q.K = d; q.epi = EPI_QKV_FRAG;
+    q.vt = h16("vt"); q.qk_cols = 2 * d; q.vt_ld = T; q.head_dim = sp.head_dim;
+    q.tile = 1; q.split = 1;   // 128x128 tiles, two K-groups when K allows
     add_gemm(b + "qkv", "gemm_qkv", q);
     const half_t* qk = h16("qk");
     const half_t* vt = h16("vt");
     half_t* att = h16("att");
     const int nh = sp.n_heads, hd = sp.head_dim, Tt = T;
     add(b + "attn", "attention", 4.0 * Tt * Tt * d, (double)Tt * d * 2 * 4, [=](hipStream_t s) {
-      launch_attention(qk, vt, att, Tt, nh, hd, s);
+      launch_attention(qk, vt, att, Tt, nh, hd, true, s);
     });
     GemmDesc o;
     o.A = att; o.lda = d; o.B = h16(p + "o.w"); o.ldb = d;

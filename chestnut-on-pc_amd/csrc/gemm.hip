@@ -43,6 +43,8 @@ struct GemmParams {
   int M, N, K, kps;   // kps: K per split
   int split, batch, Mt, Nt;
   int qk_cols;
+  int head_dim;       // EPI_QKV_FRAG
+  int vec;            // 1: shapes/alignment allow the LDS-staged 16-byte epilogue
 };
 
 template <int EPI>
@@ -58,7 +60,9 @@ __device__ __forceinline__ void epi_store(const GemmParams& p, void* C, const fl
     if (bias) v += bias[n];
     if (EPI == EPI_F16_BIAS_RELU) v = fmaxf(v, 0.f);
     if (EPI == EPI_F16_BIAS_GELU) v = gelu_fast(v);
-    if (EPI == EPI_QKV && n >= p.qk_cols) {
+    if (EPI == EPI_QKV_FRAG) {
+      return;   // unreachable: the host admits EPI_QKV_FRAG only with the staged epilogue
+    } else if (EPI == EPI_QKV && n >= p.qk_cols) {
       p.vt[(long)(n - p.qk_cols) * p.vt_ld + m] = (half_t)v;
     } else {
       static_cast<half_t*>(C)[(long)m * p.ldc + n] = (half_t)v;
@@ -293,6 +297,155 @@ __device__ __forceinline__ void dma_issue(const half_t* const* asrc, const half_
                                      0);
 }
 
+// Coalesced epilogue.  The MFMA accumulator layout gives a lane one column
+// and scattered rows, so direct stores are 2- or 4-byte pieces spread over
+// 32 rows per instruction (and, for the transposed V of the QKV epilogue,
+// over 32 V^T rows).  Instead each wave puts its finished (WM x WN) sub-tile
+// -- bias and activation applied, converted to the output type -- into a
+// private LDS region and writes it out as whole 16-byte row chunks.  V
+// columns are staged transposed ([n][m]), four consecutive rows of a lane
+// forming one 8-byte LDS write, so V^T rows leave contiguously as well.
+// Row pitches carry 16 bytes of padding so the two half-waves' staging
+// writes (rows r and r+4) fall in different banks.
+// Requires (checked on the host, else the direct per-element stores run):
+// N % 8 == 0, ldc / batch stride / base of C and ws 16-byte compatible,
+// and for QKV qk_cols % BN == 0, M % 8 == 0 and vt_ld % 8 == 0.
+//
+// EPI_QKV_FRAG writes the attention kernel's MFMA operands directly, in
+// 16-byte chunks ordered so that one wave's fragment load is one contiguous
+// KB (16 lanes x 16 B per row of the fragment would otherwise touch 16
+// separate rows).  With T = M tokens, d = qk_cols / 2, hd = head_dim,
+// H = d / hd, chunk c of a fragment holds 8 halves for lane l = 16*g + r:
+//   Q, K (16x16x32 A/B operand: row r = token, 8 head dims from 8*g):
+//     C chunk (((w*H + h) * T/16 + t/16) * hd/32 + j/32) * 64 + 16*((j%32)/8) + t%16
+//     for token t, head dim j of head h; w = 0 for Q, 1 for K.
+//   V (B operand of P.V: column r = head dim, 8 tokens from 8*g):
+//     vt chunk ((h * hd/16 + j/16) * T/32 + t/32) * 64 + 16*((t%32)/8) + j%16.
+template <int WM, int WN, int FM, int FN, int EPI>
+__device__ __forceinline__ void store_staged(const GemmParams& p, const float16_t (&acc)[FM][FN], char* region,
+                                             int mw, int nw, int sp, int bz, int lane) {
+  const bool to_ws = p.split > 1 || EPI == EPI_PARTIALS;
+  const float* bias = (!to_ws && p.bias) ? p.bias + bz * p.sBias : nullptr;
+  if (to_ws || EPI == EPI_F32 || EPI == EPI_F32_RESID) {
+    constexpr int PF = WN + 8;   // floats
+    float* st = reinterpret_cast<float*>(region);
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      const int c = j * 32 + (lane & 31);
+      const float bv = bias && nw + c < p.N ? bias[nw + c] : 0.f;
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int e = 0; e < 16; ++e)
+          st[(i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3)) * PF + c] = acc[i][j][e] + bv;
+    }
+    __builtin_amdgcn_wave_barrier();
+    asm volatile("" ::: "memory");
+    constexpr int CPR = WN / 4;   // 16-byte chunks per row
+    float* dst = to_ws ? p.ws + ((long)sp * p.batch + bz) * (long)p.M * p.N : static_cast<float*>(p.C) + bz * p.sC;
+    const long ld = to_ws ? p.N : p.ldc;
+#pragma unroll 4
+    for (int q = lane; q < WM * CPR; q += 64) {
+      const int r = q / CPR, c = (q % CPR) * 4;
+      const int m = mw + r, n = nw + c;
+      if (m >= p.M || n >= p.N) continue;
+      float4_t v = *reinterpret_cast<const float4_t*>(st + r * PF + c);
+      float4_t* g = reinterpret_cast<float4_t*>(dst + (long)m * ld + n);
+      if (!to_ws && EPI == EPI_F32_RESID) v += *g;
+      *g = v;
+    }
+    return;
+  }
+  half_t* st = reinterpret_cast<half_t*>(region);
+  if ((EPI == EPI_QKV || EPI == EPI_QKV_FRAG) && nw >= p.qk_cols) {
+    constexpr int PT = WM + 8;   // halves, transposed rows [n][m]
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      const int c = j * 32 + (lane & 31);
+      const float bv = bias && nw + c < p.N ? bias[nw + c] : 0.f;
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int g4 = 0; g4 < 4; ++g4) {
+          half4_t h;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) h[e] = (half_t)(acc[i][j][4 * g4 + e] + bv);
+          *reinterpret_cast<half4_t*>(st + c * PT + i * 32 + 8 * g4 + 4 * (lane >> 5)) = h;
+        }
+    }
+    __builtin_amdgcn_wave_barrier();
+    asm volatile("" ::: "memory");
+    if (EPI == EPI_QKV_FRAG) {
+      // V fragment blocks: 16 features x 32 tokens = 64 lanes x 8 tokens, one
+      // contiguous KB per block (see the layout note at the epilogue modes)
+      const int r = lane & 15, g = lane >> 4, HDh = p.head_dim;
+#pragma unroll
+      for (int blk = 0; blk < (WN / 16) * (WM / 32); ++blk) {
+        const int cb = blk % (WN / 16), tb = blk / (WN / 16);
+        if (mw + tb * 32 >= p.M) continue;
+        const int nl = cb * 16 + r, ml = tb * 32 + g * 8;
+        const int f = nw + nl - p.qk_cols, m = mw + ml;
+        const int h = f / HDh, c = f % HDh;
+        const long chunk = ((long)(h * (HDh / 16) + c / 16) * (p.M / 32) + m / 32) * 64 + g * 16 + r;
+        *reinterpret_cast<half8_t*>(p.vt + chunk * 8) = *reinterpret_cast<const half8_t*>(st + nl * PT + ml);
+      }
+      return;
+    }
+    constexpr int CPR = WM / 8;
+#pragma unroll 4
+    for (int q = lane; q < WN * CPR; q += 64) {
+      const int r = q / CPR, c = (q % CPR) * 8;
+      const int n = nw + r, m = mw + c;
+      if (n >= p.N || m >= p.M) continue;
+      *reinterpret_cast<half8_t*>(p.vt + (long)(n - p.qk_cols) * p.vt_ld + m) =
+          *reinterpret_cast<const half8_t*>(st + r * PT + c);
+    }
+    return;
+  }
+  constexpr int PH = WN + 8;   // halves
+#pragma unroll
+  for (int j = 0; j < FN; ++j) {
+    const int c = j * 32 + (lane & 31);
+    const float bv = bias && nw + c < p.N ? bias[nw + c] : 0.f;
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        float v = acc[i][j][e] + bv;
+        if (EPI == EPI_F16_BIAS_RELU) v = fmaxf(v, 0.f);
+        if (EPI == EPI_F16_BIAS_GELU) v = gelu_fast(v);
+        st[(i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3)) * PH + c] = (half_t)v;
+      }
+  }
+  __builtin_amdgcn_wave_barrier();
+  asm volatile("" ::: "memory");
+  if (EPI == EPI_QKV_FRAG) {
+    // Q / K fragment blocks: 16 tokens x 32 features = 64 lanes x 8 features
+    const int r = lane & 15, g = lane >> 4, HDh = p.head_dim, dh = p.qk_cols / 2, H = dh / HDh;
+#pragma unroll
+    for (int blk = 0; blk < (WM / 16) * (WN / 32); ++blk) {
+      const int tb = blk % (WM / 16), kb = blk / (WM / 16);
+      if (mw + tb * 16 >= p.M) continue;
+      const int ml = tb * 16 + r, nl = kb * 32 + g * 8;
+      const int m = mw + ml, n = nw + nl;
+      const int which = n / dh, f = n % dh, h = f / HDh, c = f % HDh;
+      const long chunk = (((long)(which * H + h) * (p.M / 16) + m / 16) * (HDh / 32) + c / 32) * 64 + g * 16 + r;
+      *reinterpret_cast<half8_t*>(static_cast<half_t*>(p.C) + chunk * 8) =
+          *reinterpret_cast<const half8_t*>(st + ml * PH + nl);
+    }
+    return;
+  }
+  constexpr int CPR = WN / 8;
+  half_t* dst = static_cast<half_t*>(p.C) + bz * p.sC;
+#pragma unroll 4
+  for (int q = lane; q < WM * CPR; q += 64) {
+    const int r = q / CPR, c = (q % CPR) * 8;
+    const int m = mw + r, n = nw + c;
+    if (m >= p.M || n >= p.N) continue;
+    *reinterpret_cast<half8_t*>(dst + (long)m * p.ldc + n) = *reinterpret_cast<const half8_t*>(st + r * PH + c);
+  }
+}
+
 // KG K-groups of 4 waves each (256*KG threads): group g consumes K-steps
 // g, g+KG, g+2KG, ... through its own S/KG stages of the ring, so KG=2 puts
 // 8 waves on a CU for one output tile (twice the loads in flight) without a
@@ -414,13 +567,30 @@ __global__ __launch_bounds__(256 * KG) void gemm_dma_kernel(const GemmParams p) 
     }
     wait_vm_lgkm0<0>();
     lds_barrier();
+    if (grp == 0) {
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) acc[i][j][e] += red[((w4 * FM * FN + i * FN + j) * 16 + e) * 64 + lane];
+    }
+    if (p.vec) {   // the staged epilogue reuses the LDS that group 0 just read
+      wait_vm_lgkm0<0>();
+      lds_barrier();
+    }
     if (grp == 1) return;   // no barrier follows
-#pragma unroll
-    for (int i = 0; i < FM; ++i)
-#pragma unroll
-      for (int j = 0; j < FN; ++j)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) acc[i][j][e] += red[((w4 * FM * FN + i * FN + j) * 16 + e) * 64 + lane];
+  } else if (p.vec) {       // every wave is past its last ring read
+    wait_vm_lgkm0<0>();
+    lds_barrier();
+  }
+
+  if (p.vec) {
+    constexpr int REGION = WM * (WN + 8) * 4;   // bytes per wave; the f32 staging is the largest
+    static_assert(4 * REGION <= S * STAGE * 2, "LDS ring too small for the staged epilogue");
+    store_staged<WM, WN, FM, FN, EPI>(p, acc, reinterpret_cast<char*>(lds) + w4 * REGION, m0 + wm * WM,
+                                      n0 + wn * WN, sp, bz, lane);
+    return;
   }
 
   if (p.split > 1 || EPI == EPI_PARTIALS) {
@@ -549,11 +719,13 @@ void launch_gemm(GemmDesc d, hipStream_t s) {
   }
   // QKV: only the first qk_cols columns are stored row-major in C
   if (d.epi != EPI_PARTIALS)
-    CK_REQUIRE(d.ldc >= (d.epi == EPI_QKV ? d.qk_cols : d.N), "gemm: ldc must be >= N (>= qk_cols for QKV)");
+    CK_REQUIRE(d.ldc >= ((d.epi == EPI_QKV || d.epi == EPI_QKV_FRAG) ? d.qk_cols : d.N),
+               "gemm: ldc must be >= N (>= qk_cols for QKV)");
   CK_REQUIRE((reinterpret_cast<uintptr_t>(d.A) & 15) == 0 && (reinterpret_cast<uintptr_t>(d.B) & 15) == 0,
              "gemm: A and B must be 16-byte aligned");
   CK_REQUIRE(d.sA % 8 == 0 && d.sB % 8 == 0, "gemm: batch strides must keep 16-byte alignment");
-  if (d.epi == EPI_QKV) CK_REQUIRE(d.vt && d.qk_cols > 0 && d.qk_cols < d.N && d.vt_ld >= d.M, "gemm: bad QKV split");
+  if (d.epi == EPI_QKV || d.epi == EPI_QKV_FRAG)
+    CK_REQUIRE(d.vt && d.qk_cols > 0 && d.qk_cols < d.N && d.vt_ld >= d.M, "gemm: bad QKV split");
   if (need) CK_REQUIRE(d.ws && d.ws_floats >= need, "gemm: split-K workspace missing or too small");
   CK_REQUIRE((long)d.M * d.lda < (1L << 31) * 8, "gemm: A too large");
 
@@ -564,6 +736,29 @@ void launch_gemm(GemmDesc d, hipStream_t s) {
   p.M = d.M; p.N = d.N; p.K = d.K; p.split = d.split; p.kps = d.K / d.split; p.batch = d.batch;
   p.Mt = ceil_div(d.M, tile_bm(d.tile)); p.Nt = ceil_div(d.N, tile_bn(d.tile));
   p.qk_cols = d.qk_cols;
+  p.head_dim = d.head_dim;
+  {
+    // the staged epilogue writes 16-byte chunks: 8 halves / 4 floats per chunk
+    const auto al16 = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
+    bool v = !d.b_kn && d.N % 8 == 0;
+    if (d.split > 1 || d.epi == EPI_PARTIALS) {
+      v = v && al16(d.ws);
+    } else {
+      const int el = (d.epi == EPI_F32 || d.epi == EPI_F32_RESID) ? 4 : 8;
+      v = v && al16(d.C) && d.ldc % el == 0 && d.sC % el == 0;
+      if (d.epi == EPI_QKV || d.epi == EPI_QKV_FRAG)
+        v = v && d.qk_cols % tile_bn(d.tile) == 0 && d.M % 8 == 0 && d.vt_ld % 8 == 0 && al16(d.vt);
+    }
+    p.vec = v ? 1 : 0;
+  }
+  if (d.epi == EPI_QKV_FRAG) {
+    const int dh = d.qk_cols / 2;
+    CK_REQUIRE(d.head_dim > 0 && d.head_dim % 32 == 0 && d.qk_cols % 2 == 0 && dh % d.head_dim == 0 &&
+                   d.N == 3 * dh && d.M % 32 == 0 && d.N % tile_bn(d.tile) == 0,
+               "gemm: QKV fragment epilogue needs N = 3d, d % head_dim == 0, head_dim % 32 == 0, M % 32 == 0");
+    CK_REQUIRE(d.split == 1 && d.batch == 1 && d.tile < 10 && p.vec,
+               "gemm: QKV fragment epilogue needs split 1, batch 1, an LDS-DMA tile and aligned outputs");
+  }
   if (d.b_kn) {
     launch_epi<true, EPI_F32>(d.tile, p, s);
     if (d.split > 1) launch_reduce<EPI_F32>(p, s);
@@ -577,6 +772,7 @@ void launch_gemm(GemmDesc d, hipStream_t s) {
     case EPI_F32_RESID: launch_epi<false, EPI_F32_RESID>(d.tile, p, s); if (d.split > 1) launch_reduce<EPI_F32_RESID>(p, s); break;
     case EPI_QKV: launch_epi<false, EPI_QKV>(d.tile, p, s); if (d.split > 1) launch_reduce<EPI_QKV>(p, s); break;
     case EPI_PARTIALS: launch_epi<false, EPI_PARTIALS>(d.tile, p, s); break;
+    case EPI_QKV_FRAG: launch_epi<false, EPI_QKV_FRAG>(d.tile, p, s); break;
     default: throw Error("gemm: unknown epilogue");
   }
 }

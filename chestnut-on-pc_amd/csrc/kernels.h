@@ -25,6 +25,9 @@ enum Epi {
   EPI_QKV = 5,            // f16(acc + bias): n < qk_cols -> C16[m][n], else vt[n-qk_cols][m]
   EPI_PARTIALS = 6,       // raw f32 acc of split s -> ws[s][M][N] (no bias, no reduce); a
                           // consumer (the residual-add LayerNorm) sums the splits
+  EPI_QKV_FRAG = 7,       // f16(acc + bias) of a [T][3d] QKV product, written in the MFMA
+                          // fragment order the attention kernel loads (see gemm.hip):
+                          // Q, K -> C, V -> vt.  Needs head_dim, M % 32 == 0, split 1.
 };
 
 struct GemmDesc {
@@ -45,6 +48,7 @@ struct GemmDesc {
   int qk_cols = 0;
   long vt_ld = 0;
   int tile = 0;                // 0 auto; else 1:128x128 2:128x64 3:64x128 4:64x64
+  int head_dim = 0;            // EPI_QKV_FRAG only
 };
 // Resolves auto tile/split (writes them back) and returns the workspace the
 // launch needs, in floats.
@@ -52,9 +56,11 @@ size_t gemm_plan(GemmDesc& d);
 void launch_gemm(GemmDesc d, hipStream_t s);
 
 // ---- attention ---------------------------------------------------------------
-// qk f16 [T][2d] (q | k, head h at columns h*hd), vt f16 [d][T] (V transposed),
-// out f16 [T][d].  Non-causal softmax(q k^T * scale) v per head.
-void launch_attention(const half_t* qk, const half_t* vt, half_t* out, int T, int n_heads, int head_dim,
+// Row layout (frag = false): qk f16 [T][2d] (q | k, head h at columns h*hd),
+// vt f16 [d][T] (V transposed).  Fragment layout (frag = true): qk and vt as
+// written by the EPI_QKV_FRAG GEMM epilogue.  out f16 [T][d].
+// Non-causal softmax(q k^T * scale) v per head.
+void launch_attention(const half_t* qk, const half_t* vt, half_t* out, int T, int n_heads, int head_dim, bool frag,
                       hipStream_t s);
 
 // ---- normalisation / small elementwise ---------------------------------------

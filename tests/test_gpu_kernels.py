@@ -166,7 +166,9 @@ def test_gemm_matches_kchain_semantics(gpu):
 
 
 @pytest.mark.parametrize('tile', [1, 2, 3, 4])
-@pytest.mark.parametrize('M,N,Kd,split', [(200, 136, 192, 1), (64, 64, 64, 1), (300, 520, 1024, 2), (33, 1000, 512, 4)])
+# N % 8 == 0 takes the LDS-staged 16-byte epilogue, N = 100 the per-element one
+@pytest.mark.parametrize('M,N,Kd,split', [(200, 136, 192, 1), (64, 64, 64, 1), (300, 520, 1024, 2), (33, 1000, 512, 4),
+                                          (72, 100, 128, 1)])
 def test_gemm_nt_tiles_tails(gpu, tile, M, N, Kd, split):
     from chestnut import kernels as K
     rng = np.random.default_rng(M * N + Kd + tile)
@@ -176,12 +178,13 @@ def test_gemm_nt_tiles_tails(gpu, tile, M, N, Kd, split):
     _gemm_check(C, A, W, transB=True)
 
 
+@pytest.mark.parametrize('N', [200, 196])
 @pytest.mark.parametrize('epi', [1, 2, 3, 4])
-def test_gemm_epilogues(gpu, epi):
+def test_gemm_epilogues(gpu, epi, N):
     from chestnut import kernels as K
     torch = gpu
     rng = np.random.default_rng(epi)
-    M, N, Kd = 96, 200, 256
+    M, Kd = 96, 256
     A = (rng.standard_normal((M, Kd)) / 8).astype(np.float16)
     W = (rng.standard_normal((N, Kd)) / 8).astype(np.float16)
     b = rng.standard_normal(N).astype(np.float32)
@@ -249,7 +252,7 @@ def test_img_gather_random_oob(gpu, dtype, lanes):
 
 
 # ------------------------------------------------ attention / layernorm ----
-@pytest.mark.parametrize('T,H,hd', [(512, 16, 128), (256, 8, 64), (64, 2, 64)])
+@pytest.mark.parametrize('T,H,hd', [(512, 16, 128), (256, 8, 64), (64, 2, 64), (192, 3, 128), (384, 5, 64)])
 def test_attention_vs_oracle(gpu, T, H, hd):
     from chestnut import kernels as K
     rng = np.random.default_rng(T + H)
