@@ -4,7 +4,8 @@ on one MI355X, replayed as one hipGraph per frame, plus per-kernel roofline
 fractions and the CPU oracle timed on the same host.
 
     python bench.py [--gpus 1] [--steps 50] [--warmup 5] [--spec big_driving_1b]
-                    [--cpu-frames 1] [--no-cpu] [--no-micro]
+                    [--cpu-frames 3] [--no-cpu] [--no-micro]
+                    [--dump-plan PATH] [--pmc-run FAMILY [--pmc-reps N] [--pmc-out PATH]]
 
 A step is one frame: inputs (uint8 frame pair + packed f32 vector) already
 resident in HBM, one hipGraph launch of the whole plan (queues, conv stem,
@@ -113,6 +114,22 @@ def micro(torch):
     return res
 
 
+def traffic_record(spec_name, fam):
+    """HBM bytes per launch of plan family `fam` from the committed PMC
+    summary (FETCH_SIZE + WRITE_SIZE passes, copy-calibrated), if one exists
+    for this family."""
+    path = os.path.join(ROOT, 'profiles', f'traffic_{spec_name}.json')
+    try:
+        with open(path) as fh:
+            t = json.load(fh)
+    except (OSError, ValueError):
+        return None
+    for e in t.get('entries', []):
+        if e.get('family') == fam:
+            return dict(e, source=os.path.relpath(path, ROOT))
+    return None
+
+
 def cpu_baseline(sp, weights, n_frames, warped, packed):
     """The numpy oracle (f32 OpenBLAS) on this host's cores, bounded sample."""
     from threadpoolctl import threadpool_limits
@@ -143,9 +160,15 @@ def main():
     ap.add_argument('--steps', type=int, default=50)
     ap.add_argument('--warmup', type=int, default=5)
     ap.add_argument('--spec', default='big_driving_1b')
-    ap.add_argument('--cpu-frames', type=int, default=1)
+    ap.add_argument('--cpu-frames', type=int, default=3)
     ap.add_argument('--no-cpu', action='store_true')
     ap.add_argument('--no-micro', action='store_true')
+    ap.add_argument('--dump-plan', default=None, help='write the frame plan (name, kernel, flops, bytes) as JSON')
+    ap.add_argument('--pmc-run', default=None, metavar='FAMILY',
+                    help='counter run: one frame, a 256 MiB device copy, then the first plan entry of each '
+                         'comma-separated FAMILY alone --pmc-reps times; writes --pmc-out and exits')
+    ap.add_argument('--pmc-reps', type=int, default=10)
+    ap.add_argument('--pmc-out', default='gpurun_out/pmc_run.json')
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get('WORLD_SIZE', '1')) != 1:
         sys.exit('bench.py measures one GPU only: this build has no multi-GPU path '
@@ -170,6 +193,31 @@ def main():
     out = eng.run_frame(warped, packed)
     log(f'[bench] first frame (capture + run) {time.perf_counter() - t0:.3f}s, graph nodes {eng.graph_nodes()}, '
         f'finite={bool(np.all(np.isfinite(out)))}')
+    if a.dump_plan:
+        with open(a.dump_plan, 'w') as fh:
+            json.dump(eng.plan(), fh)
+    if a.pmc_run:
+        plan = eng.plan()
+        nbytes = 256 << 20
+        src = torch.ones(nbytes, dtype=torch.uint8, device='cuda')
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        entries = []
+        for fam in a.pmc_run.split(','):
+            idx = next(i for i, e in enumerate(plan) if family(e['name']) == fam)
+            for _ in range(a.pmc_reps):
+                eng.run_range(idx, idx + 1)
+            eng.synchronize()
+            entries.append({'entry': plan[idx]['name'], 'index': idx, 'algorithmic_bytes': plan[idx]['bytes']})
+        info = {'entries': entries, 'reps': a.pmc_reps, 'copy_bytes': nbytes}
+        os.makedirs(os.path.dirname(os.path.abspath(a.pmc_out)), exist_ok=True)
+        with open(a.pmc_out, 'w') as fh:
+            json.dump(info, fh)
+        log(f'[bench] pmc run {info}')
+        eng.close()
+        return
     pk = packed.copy()
     n_host = 20
     t0 = time.perf_counter()
@@ -217,6 +265,10 @@ def main():
             'peak': peak, 'unit': unit, 'frac': round(ach / peak, 4), 'traffic': None,
             'us_per_launch': round(ms * 1e3, 2), 'launches_timed': len(idx) * reps,
             'algorithmic_per_launch': dom['flops'] if dom['bound'] == 'mfma' else dom['bytes']}
+    tr = traffic_record(sp['name'], dom['name'])
+    if tr:
+        roof['traffic'] = tr['traffic_bytes']
+        roof['traffic_source'] = tr['source']
 
     line = {'metric': METRIC, 'value': round(fps, 2), 'unit': 'frames/s', 'n_gpus': 1, 'steps': a.steps,
             'warmup': a.warmup, 'ms_per_step': round(wall * 1e3 / a.steps, 4), 'higher_is_better': True,

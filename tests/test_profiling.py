@@ -1,0 +1,80 @@
+"""Host logic of chestnut.profiling on synthetic rocprofv3 CSVs (no GPU)."""
+import csv
+import json
+
+from chestnut import profiling as P
+
+PLAN = [
+    {'name': 'inputs', 'kernel': 'policy_inputs', 'flops': 0, 'bytes': 10},
+    {'name': 'stem0.conv', 'kernel': 'gemm_conv_relu+splitk2', 'flops': 4, 'bytes': 20},
+    {'name': 'blk0.o', 'kernel': 'gemm_partials+splitk4', 'flops': 8, 'bytes': 30},
+    {'name': 'blk0.ln2', 'kernel': 'add_layernorm_f16', 'flops': 0, 'bytes': 40},
+    {'name': 'blk1.o', 'kernel': 'gemm_partials+splitk4', 'flops': 8, 'bytes': 30},
+    {'name': 'tick', 'kernel': 'frame_tick', 'flops': 0, 'bytes': 4},
+]
+FRAME = [('ck::policy_inputs_kernel(args)', 1.0), ('gemm_dma_kernel<64, 64, 5, 1, 2>', 2.0),
+         ('splitk_reduce_kernel<2>', 0.5), ('gemm_dma_kernel<128, 128, 4, 2, 6>', 3.0),
+         ('layernorm_row_kernel<8, true, true>', 4.0), ('gemm_dma_kernel<128, 128, 4, 2, 6>', 5.0),
+         ('frame_tick_kernel', 0.25)]
+
+
+def _trace_csv(path, seq):
+    with open(path, 'w', newline='') as fh:
+        w = csv.writer(fh)
+        w.writerow(['Kernel_Name', 'Start_Timestamp', 'End_Timestamp'])
+        t = 1000
+        for name, us in seq:
+            w.writerow([name, t, t + int(us * 1000)])
+            t += int(us * 1000) + 100
+
+
+def test_frames_follow_plan_order(tmp_path):
+    # noise before, a family-timing loop (inputs twice) between, two real frames
+    seq = [('fillBuffer', 1.0)] + FRAME + [('ck::policy_inputs_kernel(args)', 1.0)] * 2 + FRAME
+    _trace_csv(tmp_path / 't.csv', seq)
+    frames = P.frames_from_trace(P.load_trace(tmp_path / 't.csv'), PLAN)
+    assert len(frames) == 2
+    assert frames[0] == [1.0, 2.5, 3.0, 4.0, 5.0, 0.25]   # the reduce belongs to stem0.conv
+
+
+def test_frames_reject_mismatch(tmp_path):
+    bad = FRAME[:4] + [('attention_kernel', 1.0)] + FRAME[5:]
+    _trace_csv(tmp_path / 't.csv', bad)
+    assert P.frames_from_trace(P.load_trace(tmp_path / 't.csv'), PLAN) == []
+
+
+def test_frames_md_families(tmp_path):
+    _trace_csv(tmp_path / 't.csv', FRAME)
+    with open(tmp_path / 's.csv', 'w', newline='') as fh:
+        w = csv.writer(fh)
+        w.writerow(['Name', 'Calls', 'AverageNs', 'MinNs', 'MaxNs', 'Percentage'])
+        w.writerow(['gemm_dma_kernel', 3, 3000, 2000, 5000, 60.0])
+    json.dump(PLAN, open(tmp_path / 'p.json', 'w'))
+    md = P.frames_md(tmp_path / 't.csv', tmp_path / 's.csv', tmp_path / 'p.json', 'cmd')
+    assert '| blk.o | gemm_partials+splitk4 | 2 | 4.00 | 3.00 | 8.0 |' in md
+
+
+def _counter_csv(path, counter, seq):
+    with open(path, 'w', newline='') as fh:
+        w = csv.writer(fh)
+        w.writerow(['Dispatch_Id', 'Kernel_Name', 'Counter_Name', 'Counter_Value'])
+        for i, (name, v) in enumerate(seq):
+            w.writerow([i + 1, name, counter, v])
+
+
+def test_traffic_calibration(tmp_path):
+    # copy of 1 MiB reads as 512 KiB fetched (factor 2) and 1024 KiB written (factor 1)
+    fetch = [('ck::x', 1.0), ('__amd_rocclr_copyBuffer', 512.0)] + [('ck::gemm', 100.0)] * 3 + \
+            [('ck::attn', 10.0), ('ck::attn', 12.0), ('ck::attn', 11.0)]
+    write = [('ck::x', 1.0), ('__amd_rocclr_copyBuffer', 1024.0)] + [('ck::gemm', 50.0)] * 3 + \
+            [('ck::attn', 4.0)] * 3
+    _counter_csv(tmp_path / 'f.csv', 'FETCH_SIZE', fetch)
+    _counter_csv(tmp_path / 'w.csv', 'WRITE_SIZE', write)
+    run = {'reps': 3, 'copy_bytes': 1 << 20,
+           'entries': [{'entry': 'blk0.down', 'algorithmic_bytes': 1.0}, {'entry': 'blk0.attn', 'algorithmic_bytes': 2.0}]}
+    json.dump(run, open(tmp_path / 'r.json', 'w'))
+    t = P.traffic(tmp_path / 'f.csv', tmp_path / 'w.csv', tmp_path / 'r.json')
+    assert t['fetch_factor'] == 2.0 and t['write_factor'] == 1.0
+    d, a = t['entries']
+    assert d['family'] == 'blk.down' and d['traffic_bytes'] == 100 * 1024 * 2 + 50 * 1024
+    assert a['family'] == 'blk.attn' and a['read_bytes'] == 11 * 1024 * 2
