@@ -206,6 +206,31 @@ class Engine:
         arr = np.ascontiguousarray(arr)
         call('ck_write_tensor', self._h, name.encode(), arr.ctypes.data, arr.nbytes)
 
+    # -- frame state (probe pre-state capture, cf. r62_probe.py:28-44) ------------
+    def state_names(self):
+        """[(name, nbytes, numpy dtype)] of every non-parameter tensor."""
+        n = ctypes.c_int()
+        call('ck_state_count', self._h, ctypes.byref(n))
+        out = []
+        name = ctypes.create_string_buffer(256)
+        nb = ctypes.c_size_t()
+        dt = ctypes.c_int()
+        for i in range(n.value):
+            call('ck_state_info', self._h, i, name, len(name), ctypes.byref(nb), ctypes.byref(dt))
+            out.append((name.value.decode(), nb.value, _DT[dt.value]))
+        return out
+
+    def snapshot(self):
+        """Host copies of the whole frame state: {name: 1-D array}."""
+        self.synchronize()
+        return {n: self.read(n, dt) for n, _, dt in self.state_names()}
+
+    def restore(self, state):
+        """Write a snapshot back (every tensor it holds)."""
+        self.synchronize()
+        for n, a in state.items():
+            self.write(n, a)
+
 
 def load(spec='big_driving_1b', **kw):
     """The reference's exec-prefix namespace (run_pinned2.py:1346-1572):

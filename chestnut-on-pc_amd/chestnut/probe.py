@@ -1,0 +1,189 @@
+"""Per-kernel probe and A/B bench of one frame-plan entry.
+
+The reference studies one kernel at a time in two steps: a probe runs a
+real frame and dumps the kernel's pre-state buffers (r62_probe.py:1-80,
+alu_probe.py:1-60), then a bench replays that kernel on a fresh context
+15 times, baseline and variant, and prints median / min time plus
+bit-identical / ndiff / maxabs / maxrel of the variant's output against the
+baseline's (bench_r62.py:25-65).  Here:
+
+  capture   run `frames` frames of make_warped(val) (the last one only up to
+            the entry), snapshot the whole frame state (every non-parameter
+            tensor, including the split-K workspace), run the entry once and
+            snapshot again; then time the entry `reps` times, each launch on
+            a restored pre-state, between HIP events on the engine stream.
+            Writes DIR/meta.json, DIR/pre.npz, DIR/post.npz.
+
+  bench     rebuild the same engine (same spec and seeded weights) with a
+            variant -- another build of the library (--lib, the analogue of
+            the reference's variant cubin) and/or a GEMM tile/split for this
+            entry (--gemm TILE,SPLIT, the analogue of its local-size
+            argument) -- restore the captured pre-state, time the entry the
+            same way and compare every state tensor with post.npz.
+
+    python -m chestnut.probe capture --spec big_driving_1b --entry blk0.up --out DIR
+    python -m chestnut.probe bench DIR [--lib PATH] [--gemm 5,2] [--reps 15]
+
+Timings are per launch (HIP events around the single entry, no host
+launch overhead), so `med` is the kernel's own duration.
+"""
+import argparse
+import json
+import os
+import sys
+
+import numpy as np
+
+
+def _engine(spec, lib=None):
+    if lib:
+        from . import _lib
+        _lib.LIB_PATH = os.path.abspath(lib)
+    from .engine import Engine
+    from . import spec as S
+    return Engine(spec, weights=S.make_weights(spec))
+
+
+def _time_entry(eng, idx, pre, reps):
+    ts = []
+    for _ in range(reps):
+        eng.restore(pre)
+        ts.append(eng.time_launches([idx], 1))
+    return ts
+
+
+def compare(base, var):
+    """bench_r62.py:57-65 statistics over every state tensor: bit-identical,
+    number of differing elements, max abs / max rel difference over the
+    floating-point elements where the baseline is non-zero."""
+    ndiff, maxabs, maxrel = 0, 0.0, 0.0
+    changed = []
+    for name, b in base.items():
+        v = var[name]
+        if b.shape != v.shape or b.dtype != v.dtype:
+            raise ValueError(f'{name}: shape/dtype differ ({b.shape} {b.dtype} vs {v.shape} {v.dtype})')
+        diff = b.view(np.uint8).reshape(-1, b.itemsize) != v.view(np.uint8).reshape(-1, b.itemsize)
+        nd = int(diff.any(axis=1).sum())
+        if nd:
+            changed.append(name)
+        ndiff += nd
+        if b.dtype.kind == 'f':
+            b64, v64 = b.astype(np.float64), v.astype(np.float64)
+            nz = b64 != 0
+            if nz.any():
+                d = np.abs(b64[nz] - v64[nz])
+                maxabs = max(maxabs, float(np.nanmax(d)))
+                maxrel = max(maxrel, float(np.nanmax(d / np.maximum(1e-30, np.abs(b64[nz])))))
+    return {'bit_identical': ndiff == 0, 'ndiff': ndiff, 'maxabs': maxabs, 'maxrel': maxrel, 'changed': changed}
+
+
+def fmt_times(ts):
+    s = sorted(ts)
+    return f'med={s[len(s) // 2]:.4f}ms min={s[0]:.4f}ms'
+
+
+def capture(spec_name, entry, out, frames=1, val=111, reps=15, gemm=None):
+    from . import spec as S
+    sp = S.get_spec(spec_name)
+    if gemm:
+        sp = dict(sp, gemm_config={entry: list(gemm)})
+    eng = _engine(sp)
+    names = [e['name'] for e in eng.plan()]
+    if entry not in names:
+        raise SystemExit(f'unknown plan entry {entry!r}; entries: {", ".join(names)}')
+    idx = names.index(entry)
+    plan = eng.plan()[idx]
+    warped = eng.make_warped(val)
+    packed = eng.PACKED.copy()
+    packed[8:10] = (1.0, 0.0)
+    for _ in range(frames - 1):
+        o = eng.run_frame(warped, packed)
+        packed[12:] = o[eng.out_slices['hidden_state']]
+    eng.write('warped', warped)
+    eng.write('packed', packed)
+    eng.run_range(0, idx)
+    pre = eng.snapshot()
+    eng.run_range(idx, idx + 1)
+    post = eng.snapshot()
+    ts = _time_entry(eng, idx, pre, reps)
+    eng.close()
+    os.makedirs(out, exist_ok=True)
+    np.savez(os.path.join(out, 'pre.npz'), **pre)
+    np.savez(os.path.join(out, 'post.npz'), **post)
+    meta = {'spec': sp, 'entry': entry, 'index': idx, 'kernel': plan['kernel'], 'flops': plan['flops'],
+            'bytes': plan['bytes'], 'frames': frames, 'val': val, 'reps': reps, 'baseline_ms': ts,
+            'state': {k: [str(v.dtype), int(v.size)] for k, v in pre.items()}}
+    with open(os.path.join(out, 'meta.json'), 'w') as fh:
+        json.dump(meta, fh, indent=1)
+    return meta
+
+
+def bench(d, lib=None, gemm=None, reps=None):
+    meta = json.load(open(os.path.join(d, 'meta.json')))
+    sp = dict(meta['spec'])
+    if gemm:
+        sp['gemm_config'] = dict(sp.get('gemm_config', {}), **{meta['entry']: list(gemm)})
+    pre = dict(np.load(os.path.join(d, 'pre.npz')))
+    base = dict(np.load(os.path.join(d, 'post.npz')))
+    eng = _engine(sp, lib)
+    idx = [e['name'] for e in eng.plan()].index(meta['entry'])
+    if idx != meta['index']:
+        raise SystemExit('the variant plan differs from the captured one')
+    # a variant split-K factor resizes the workspace: restore its captured
+    # prefix, and leave tensors whose size changed out of the comparison
+    sizes = {n: nb // np.dtype(dt).itemsize for n, nb, dt in eng.state_names()}
+    resized = [n for n, a in pre.items() if sizes[n] != a.size]
+    for n in resized:
+        a = np.zeros(sizes[n], pre[n].dtype)
+        k = min(a.size, pre[n].size)
+        a[:k] = pre[n][:k]
+        pre[n] = a
+        del base[n]
+    eng.restore(pre)
+    eng.run_range(idx, idx + 1)
+    var = eng.snapshot()
+    ts = _time_entry(eng, idx, pre, reps or meta['reps'])
+    eng.close()
+    res = compare(base, {n: var[n] for n in base})
+    res['resized'] = resized
+    res['variant_ms'] = ts
+    res['baseline_ms'] = meta['baseline_ms']
+    return res
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser(prog='python -m chestnut.probe', description=__doc__.split('\n\n')[0])
+    sub = ap.add_subparsers(dest='cmd', required=True)
+    c = sub.add_parser('capture')
+    c.add_argument('--spec', default='big_driving_1b')
+    c.add_argument('--entry', required=True)
+    c.add_argument('--out', required=True)
+    c.add_argument('--frames', type=int, default=1)
+    c.add_argument('--val', type=int, default=111)
+    c.add_argument('--reps', type=int, default=15)
+    c.add_argument('--gemm', default=None, help='TILE,SPLIT for the entry in the baseline')
+    b = sub.add_parser('bench')
+    b.add_argument('dir')
+    b.add_argument('--lib', default=None)
+    b.add_argument('--gemm', default=None, help='TILE,SPLIT for the entry in the variant')
+    b.add_argument('--reps', type=int, default=None)
+    a = ap.parse_args(argv)
+    gemm = tuple(int(x) for x in a.gemm.split(',')) if a.gemm else None
+    if a.cmd == 'capture':
+        m = capture(a.spec, a.entry, a.out, a.frames, a.val, a.reps, gemm)
+        print(f"[probe] {m['entry']} (plan index {m['index']}, {m['kernel']}): {len(m['state'])} state tensors "
+              f"captured to {a.out}", flush=True)
+        print(f"baseline: {fmt_times(m['baseline_ms'])}", flush=True)
+    else:
+        r = bench(a.dir, a.lib, gemm, a.reps)
+        print(f"baseline: {fmt_times(r['baseline_ms'])}")
+        print(f"variant : {fmt_times(r['variant_ms'])}  bit-identical={r['bit_identical']} ndiff={r['ndiff']} "
+              f"maxabs={r['maxabs']:.3e} maxrel={r['maxrel']:.3e}", flush=True)
+        if r['changed']:
+            print(f"          differing tensors: {', '.join(r['changed'])}", flush=True)
+        if r['resized']:
+            print(f"          not compared (size differs in the variant): {', '.join(r['resized'])}", flush=True)
+
+
+if __name__ == '__main__':
+    sys.exit(main())

@@ -88,6 +88,32 @@ int ck_param_info(ck_engine* e, int i, char* name, size_t name_len, size_t* nbyt
   CK_API_END
 }
 
+int ck_state_count(ck_engine* e, int* n) {
+  CK_API_BEGIN
+  CK_REQUIRE(e && n, "null argument");
+  int c = 0;
+  for (auto& t : e->tensors) c += t.param ? 0 : 1;
+  *n = c;
+  CK_API_END
+}
+
+int ck_state_info(ck_engine* e, int i, char* name, size_t name_len, size_t* nbytes, int* dtype) {
+  CK_API_BEGIN
+  CK_REQUIRE(e, "null engine");
+  int c = 0;
+  for (auto& t : e->tensors) {
+    if (t.param) continue;
+    if (c++ == i) {
+      copy_str(t.name, name, name_len);
+      if (nbytes) *nbytes = t.nbytes;
+      if (dtype) *dtype = t.dtype;
+      return 0;
+    }
+  }
+  throw Error("ck_state_info: index out of range");
+  CK_API_END
+}
+
 int ck_upload_param(ck_engine* e, const char* name, const void* host, size_t nbytes) {
   CK_API_BEGIN
   CK_REQUIRE(e && name && host, "null argument");

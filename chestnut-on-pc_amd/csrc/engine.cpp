@@ -69,6 +69,14 @@ Spec parse_spec(const std::string& json) {
       s.outputs.emplace_back(e.arr[0].str, (int)e.arr[1].num);
     }
   }
+  if (const JVal* gc = o.get("gemm_config")) {
+    CK_REQUIRE(gc->kind == JVal::OBJ, "spec: gemm_config must be an object {entry: [tile, split]}");
+    for (const auto& kv : gc->obj) {
+      CK_REQUIRE(kv.second.kind == JVal::ARR && kv.second.arr.size() == 2,
+                 "spec: gemm_config entries are [tile, split]");
+      s.gemm_cfg.push_back({kv.first, {(int)kv.second.arr[0].num, (int)kv.second.arr[1].num}});
+    }
+  }
   // structural requirements of the kernels
   CK_REQUIRE(s.n_frames == 2, "spec: n_frames must be 2 (two sampled frames per stream)");
   CK_REQUIRE(s.d == s.n_heads * s.head_dim, "spec: d_model must equal n_heads * head_dim");
@@ -111,7 +119,6 @@ ck_engine::~ck_engine() {
   drop_graph();
   for (auto& t : tensors)
     if (t.ptr) (void)hipFree(t.ptr);
-  if (ws) (void)hipFree(ws);
   if (h_warped) (void)hipHostFree(h_warped);
   if (h_packed) (void)hipHostFree(h_packed);
   if (h_out) (void)hipHostFree(h_out);
@@ -229,7 +236,12 @@ void ck_engine::add(const std::string& name, const std::string& kernel, double f
   plan.push_back(std::move(l));
 }
 
-void ck_engine::add_gemm(const std::string& name, const std::string& kernel, GemmDesc g) {
+int ck_engine::add_gemm(const std::string& name, const std::string& kernel, GemmDesc g) {
+  for (const auto& c : sp.gemm_cfg)
+    if (c.first == name) {
+      g.tile = c.second.first;
+      g.split = c.second.second;
+    }
   const size_t need = gemm_plan(g);
   ws_floats = std::max(ws_floats, need);
   const double M = g.M, N = g.N, K = g.K, B = g.batch;
@@ -244,6 +256,7 @@ void ck_engine::add_gemm(const std::string& name, const std::string& kernel, Gem
     d.ws_floats = self->ws_floats;
     launch_gemm(d, s);
   });
+  return g.split;
 }
 
 void ck_engine::build_plan() {
@@ -386,9 +399,8 @@ void ck_engine::build_plan() {
     GemmDesc o;
     o.A = att; o.lda = d; o.B = h16(p + "o.w"); o.ldb = d;
     o.M = T; o.N = d; o.K = d; o.epi = EPI_PARTIALS; o.tile = 1; o.split = s_o;
-    add_gemm(b + "o", "gemm_partials", o);
+    pend_split = add_gemm(b + "o", "gemm_partials", o);   // the split actually used (gemm_config may set it)
     pend_bias = f32(p + "o.b");
-    pend_split = s_o;
     add_ln(b + "ln2", f32(p + "ln2.g"), f32(p + "ln2.b"), hb, true);
     GemmDesc up;
     up.A = hb; up.lda = d; up.B = h16(p + "up.w"); up.ldb = d; up.C = ptr("u"); up.ldc = F;
@@ -398,9 +410,8 @@ void ck_engine::build_plan() {
     GemmDesc dn;
     dn.A = h16("u"); dn.lda = F; dn.B = h16(p + "down.w"); dn.ldb = F;
     dn.M = T; dn.N = d; dn.K = F; dn.epi = EPI_PARTIALS; dn.tile = 1; dn.split = s_dn;
-    add_gemm(b + "down", "gemm_partials", dn);
+    pend_split = add_gemm(b + "down", "gemm_partials", dn);
     pend_bias = f32(p + "down.b");
-    pend_split = s_dn;
   }
   // 5. final LN (adds the last block's MLP partials) + pool, GRU, heads, tick
   {
@@ -437,7 +448,9 @@ void ck_engine::build_plan() {
     float* feat = f32("packed") + dl + 4;
     add("tick", "frame_tick", 0, 8.0 * Hh, [=](hipStream_t s) { launch_frame_tick(counter, hn, feat, Hh, s); });
   }
-  if (ws_floats) CK_HIP(hipMalloc((void**)&ws, ws_floats * sizeof(float)));
+  // the split-K workspace is an ordinary activation tensor ("ws"), so state
+  // snapshots (probes) see the partials a residual LayerNorm consumes
+  if (ws_floats) ws = static_cast<float*>(add_tensor("ws", ws_floats * sizeof(float), DT_F32, false).ptr);
 }
 
 void ck_engine::upload(const std::string& name, const void* host, size_t nbytes) {

@@ -22,6 +22,8 @@ struct Spec {
   float eps = 1e-5f;
   std::vector<int> stem;
   std::vector<std::pair<std::string, int>> outputs;
+  // optional per-plan-entry GEMM configuration {entry: [tile, split]} (A/B probes)
+  std::vector<std::pair<std::string, std::pair<int, int>>> gemm_cfg;
 };
 Spec parse_spec(const std::string& json);
 
@@ -87,5 +89,5 @@ struct ck_engine {
   void build_plan();
   void add(const std::string& name, const std::string& kernel, double flops, double bytes,
            std::function<void(hipStream_t)> fn);
-  void add_gemm(const std::string& name, const std::string& kernel, ck::GemmDesc g);
+  int add_gemm(const std::string& name, const std::string& kernel, ck::GemmDesc g);
 };

@@ -118,6 +118,12 @@ int ck_time_launches(ck_engine* e, const int* idx, int n, int reps, float* ms);
  * Replaces: KDUMP pre-state dumps (run_pinned2.py:1533-1545) and the
  * probes' cuMemcpyDtoH captures (r62_probe.py:28-37). */
 int ck_tensor(ck_engine* e, const char* name, void** dptr, size_t* nbytes);
+/* Frame state: the non-parameter tensors (inputs, rings, activations, the
+ * split-K workspace "ws"), in allocation order.  dtype as ck_param_info plus
+ * 2 = u8, 3 = u32.  A probe snapshots all of them around one plan entry.
+ * Replaces: the probes' per-argument span discovery (r62_probe.py:31-35). */
+int ck_state_count(ck_engine* e, int* n);
+int ck_state_info(ck_engine* e, int i, char* name, size_t name_len, size_t* nbytes, int* dtype);
 int ck_read_tensor(ck_engine* e, const char* name, void* host, size_t nbytes);
 int ck_write_tensor(ck_engine* e, const char* name, const void* host, size_t nbytes);
 
