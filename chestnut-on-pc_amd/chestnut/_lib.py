@@ -43,6 +43,7 @@ _SIGS = {
     'ck_time_launches': (c_int, [c_void_p, P(c_int), c_int, c_int, P(c_float)]),
     'ck_tensor': (c_int, [c_void_p, c_char_p, P(c_void_p), P(c_size_t)]),
     'ck_state_count': (c_int, [c_void_p, P(c_int)]),
+    'ck_decoded_layout': (c_int, [c_void_p, P(c_int), ctypes.c_char_p, c_size_t]),
     'ck_state_info': (c_int, [c_void_p, c_int, ctypes.c_char_p, c_size_t, P(c_size_t), P(c_int)]),
     'ck_read_tensor': (c_int, [c_void_p, c_char_p, c_void_p, c_size_t]),
     'ck_write_tensor': (c_int, [c_void_p, c_char_p, c_void_p, c_size_t]),

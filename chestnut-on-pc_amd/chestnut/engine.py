@@ -42,6 +42,9 @@ class Engine:
             buf = ctypes.create_string_buffer(1 << 14)
             call('ck_output_slices', self._h, buf, len(buf))
             self.out_slices = {k: slice(v[0], v[1]) for k, v in json.loads(buf.value.decode()).items()}
+            lbuf = ctypes.create_string_buffer(1 << 16)
+            call('ck_decoded_layout', self._h, None, lbuf, len(lbuf))
+            self.decoded_layout = json.loads(lbuf.value.decode())
             self.set_graph(graph)
         except Exception:
             self.close()
@@ -205,6 +208,13 @@ class Engine:
     def write(self, name, arr):
         arr = np.ascontiguousarray(arr)
         call('ck_write_tensor', self._h, name.encode(), arr.ctypes.data, arr.nbytes)
+
+    def parsed_outputs(self):
+        """The Parser's output dictionary (parse_model_outputs.py:117-120) of
+        the last frame, from the device decode that ends every frame."""
+        from .parse import assemble
+        self.synchronize()
+        return assemble(self.read('decoded', np.float32), self.decoded_layout)
 
     # -- frame state (probe pre-state capture, cf. r62_probe.py:28-44) ------------
     def state_names(self):

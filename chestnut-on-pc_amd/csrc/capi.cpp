@@ -129,6 +129,14 @@ int ck_output_size(ck_engine* e, int* n) {
   CK_API_END
 }
 
+int ck_decoded_layout(ck_engine* e, int* n, char* buf, size_t len) {
+  CK_API_BEGIN
+  CK_REQUIRE(e, "null engine");
+  if (n) *n = e->n_decoded;
+  if (buf) copy_str(e->dec_layout, buf, len);
+  CK_API_END
+}
+
 int ck_output_slices(ck_engine* e, char* buf, size_t len) {
   CK_API_BEGIN
   CK_REQUIRE(e, "null engine");

@@ -107,6 +107,7 @@ ck_engine::ck_engine(const std::string& spec_json) : sp(parse_spec(spec_json)) {
   CK_HIP(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking));
   build_params();
   build_activations();
+  build_decode();
   build_plan();
   CK_HIP(hipHostMalloc((void**)&h_warped, warped_bytes, hipHostMallocDefault));
   CK_HIP(hipHostMalloc((void**)&h_packed, packed_len * sizeof(float), hipHostMallocDefault));
@@ -119,6 +120,7 @@ ck_engine::~ck_engine() {
   drop_graph();
   for (auto& t : tensors)
     if (t.ptr) (void)hipFree(t.ptr);
+  if (dec_dev) (void)hipFree(dec_dev);
   if (h_warped) (void)hipHostFree(h_warped);
   if (h_packed) (void)hipHostFree(h_packed);
   if (h_out) (void)hipHostFree(h_out);
@@ -185,6 +187,111 @@ void ck_engine::build_params() {
   f16("gru.wih", 3L * Hh * d); f32("gru.bih", 3L * Hh);
   f16("gru.whh", 3L * Hh * Hh); f32("gru.bhh", 3L * Hh);
   f16("head.w", (long)n_head_out * Hh); f32("head.b", n_head_out);
+}
+
+// Output decode table: each output head gets the Parser's treatment by name
+// (parse_model_outputs.py:95-120); heads it does not parse (hidden_state,
+// unknown names) pass through.  The decoded vector's layout is published as
+// JSON (ck_decoded_layout).
+void ck_engine::build_decode() {
+  struct Rule {
+    const char* name;
+    int kind, width;
+  };
+  static const Rule rules[] = {
+      {"pose", DEC_MDN, 0},           {"wide_from_device_euler", DEC_MDN, 0}, {"road_transform", DEC_MDN, 0},
+      {"lane_lines", DEC_MDN, 0},     {"road_edges", DEC_MDN, 0},             {"plan", DEC_MDN, 0},
+      {"lead", DEC_MDN, 0},           {"lane_lines_prob", DEC_SIGMOID, 0},    {"meta", DEC_SIGMOID, 0},
+      {"lead_prob", DEC_SIGMOID, 0},  {"desire_pred", DEC_SOFTMAX, 8},        {"desire_state", DEC_SOFTMAX, 8}};
+  // lead is multi-hypothesis (2 hypotheses, 3 selections) unless it holds
+  // exactly 2 x 3 selections x 6 steps x 4 values (is_mhp, parse_model_outputs.py:88-93, 105-109)
+  constexpr int LEAD_MDN_LEN = 2 * 3 * 6 * 4;
+  std::vector<std::pair<std::string, int>> heads(sp.outputs);
+  heads.push_back({"hidden_state", sp.hidden});
+  std::ostringstream js;
+  auto range = [&](const char* key, int a, int b) { js << "\"" << key << "\":[" << a << "," << b << "]"; };
+  js << "{";
+  int in_off = 0, out_off = 0;
+  for (size_t k = 0; k < heads.size(); ++k) {
+    const std::string& name = heads[k].first;
+    DecodeHead h{};
+    h.kind = DEC_RAW;
+    h.in_off = in_off;
+    h.len = heads[k].second;
+    h.out_off = out_off;
+    for (const Rule& r : rules)
+      if (name == r.name) {
+        h.kind = r.kind;
+        h.width = r.width;
+      }
+    if (name == "lead" && h.len != LEAD_MDN_LEN) {
+      h.kind = DEC_MHP;
+      h.in_N = 2;
+      h.out_N = 3;
+    }
+    int o = out_off;
+    js << (k ? "," : "") << "\"" << name << "\":{";
+    switch (h.kind) {
+      case DEC_MDN:
+        CK_REQUIRE(h.len >= 2, "decode: MDN head " + name + " needs at least 2 values");
+        h.n = h.len / 2;
+        js << "\"kind\":\"mdn\",\"n\":" << h.n << ",";
+        range("mu", o, o + h.n);
+        js << ",";
+        range("std", o + h.n, o + 2 * h.n);
+        o += 2 * h.n;
+        break;
+      case DEC_SIGMOID:
+        js << "\"kind\":\"sigmoid\",";
+        range("p", o, o + h.len);
+        o += h.len;
+        break;
+      case DEC_SOFTMAX:
+        CK_REQUIRE(h.len % h.width == 0, "decode: softmax head " + name + " is not a whole number of groups");
+        js << "\"kind\":\"softmax\",\"width\":" << h.width << ",";
+        range("p", o, o + h.len);
+        o += h.len;
+        break;
+      case DEC_MHP: {
+        const int L = h.len / h.in_N;
+        CK_REQUIRE(h.len % h.in_N == 0 && L > h.out_N && (L - h.out_N) % 2 == 0,
+                   "decode: multi-hypothesis head " + name + " does not split into [mu | std | weights]");
+        h.n = (L - h.out_N) / 2;
+        const int N = h.in_N, S = h.out_N, n = h.n;
+        js << "\"kind\":\"mhp\",\"in_N\":" << N << ",\"out_N\":" << S << ",\"n\":" << n << ",";
+        range("weights", o, o + N * S);
+        o += N * S;
+        js << ",";
+        range("hyp_mu", o, o + N * n);
+        o += N * n;
+        js << ",";
+        range("hyp_std", o, o + N * n);
+        o += N * n;
+        js << ",";
+        range("mu", o, o + S * n);
+        o += S * n;
+        js << ",";
+        range("std", o, o + S * n);
+        o += S * n;
+        break;
+      }
+      default:
+        js << "\"kind\":\"raw\",";
+        range("p", o, o + h.len);
+        o += h.len;
+        break;
+    }
+    js << "}";
+    dec_heads.push_back(h);
+    in_off += h.len;
+    out_off = o;
+  }
+  js << "}";
+  dec_layout = js.str();
+  n_decoded = out_off;
+  add_tensor("decoded", (size_t)n_decoded * 4, DT_F32, false);
+  CK_HIP(hipMalloc((void**)&dec_dev, dec_heads.size() * sizeof(DecodeHead)));
+  CK_HIP(hipMemcpy(dec_dev, dec_heads.data(), dec_heads.size() * sizeof(DecodeHead), hipMemcpyHostToDevice));
 }
 
 void ck_engine::build_activations() {
@@ -444,6 +551,10 @@ void ck_engine::build_plan() {
     add("heads", "gemv", 2.0 * nho * Hh, (double)nho * Hh * 2, [=](hipStream_t s) {
       launch_gemv(hw, hn, hbias, out, nho, Hh, Hh, GEMV_NONE, 0, s);
     });
+    float* dec = f32("decoded");
+    const DecodeHead* dd = dec_dev;
+    const int ndh = (int)dec_heads.size();
+    add("decode", "decode", 0, (double)(n_out + n_decoded) * 4, [=](hipStream_t s) { launch_decode(out, dec, dd, ndh, s); });
     unsigned* counter = static_cast<unsigned*>(ptr("counter"));
     float* feat = f32("packed") + dl + 4;
     add("tick", "frame_tick", 0, 8.0 * Hh, [=](hipStream_t s) { launch_frame_tick(counter, hn, feat, Hh, s); });

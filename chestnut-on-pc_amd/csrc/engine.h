@@ -59,6 +59,11 @@ struct ck_engine {
   size_t graph_nodes = 0;
   float* ws = nullptr;
   size_t ws_floats = 0;
+  // output decode: per-head table (host + device copy), decoded-vector layout as JSON
+  std::vector<ck::DecodeHead> dec_heads;
+  ck::DecodeHead* dec_dev = nullptr;
+  std::string dec_layout;
+  int n_decoded = 0;
   uint8_t* h_warped = nullptr;   // pinned staging (outlives every async copy)
   float* h_packed = nullptr;
   float* h_out = nullptr;
@@ -87,6 +92,7 @@ struct ck_engine {
   void build_params();
   void build_activations();
   void build_plan();
+  void build_decode();
   void add(const std::string& name, const std::string& kernel, double flops, double bytes,
            std::function<void(hipStream_t)> fn);
   int add_gemm(const std::string& name, const std::string& kernel, ck::GemmDesc g);

@@ -78,6 +78,19 @@ void launch_embed_init(const half_t* pos, const float* ctx, const float* bias, f
 void launch_frame_tick(unsigned* counter, const float* h, float* packed_feat, int H, hipStream_t s);
 void launch_fill_u32(void* p, unsigned v, size_t n_words, hipStream_t s);
 
+// ---- output decode (parse_model_outputs.py Parser on device) -----------------
+enum DecodeKind { DEC_RAW = 0, DEC_MDN = 1, DEC_SIGMOID = 2, DEC_SOFTMAX = 3, DEC_MHP = 4 };
+struct DecodeHead {
+  int kind;
+  int in_off, len;   // raw slice of the output vector
+  int out_off;       // start in the decoded vector
+  int n;             // MDN / MHP: values per mu (and per std)
+  int width;         // SOFTMAX group width
+  int in_N, out_N;   // MHP hypotheses / selections (in_N <= 8, out_N <= 8)
+};
+// One workgroup per head; heads_dev is a device copy of the table.
+void launch_decode(const float* raw, float* decoded, const DecodeHead* heads_dev, int n_heads, hipStream_t s);
+
 // ---- frame inputs, packing, image2d ------------------------------------------
 struct QueueDims {
   int img_h, img_w;          // 128, 256

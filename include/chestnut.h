@@ -64,6 +64,15 @@ int ck_upload_param(ck_engine* e, const char* name, const void* host, size_t nby
 int ck_output_size(ck_engine* e, int* n);
 int ck_output_slices(ck_engine* e, char* buf, size_t len);
 
+/* Parsed outputs.  Every frame ends with the Parser's decode on device
+ * (MDN mu / safe_exp std, sigmoid, grouped softmax, multi-hypothesis
+ * selection, by head name); the f32 result is the state tensor "decoded"
+ * (read it with ck_read_tensor).  This returns its length and its layout as
+ * JSON: {head: {"kind": "mdn"|"sigmoid"|"softmax"|"mhp"|"raw", ranges...}}.
+ * Replaces: Parser.parse_outputs on the sliced output vector
+ * (parse_model_outputs.py:95-120; modeld.py:161-162, 195). */
+int ck_decoded_layout(ck_engine* e, int* n, char* buf, size_t len);
+
 /* One policy frame.  warped: uint8 [2][6][img_h][img_w] host array;
  * packed: f32 [desire 8 | traffic_convention 2 | action_t 2 | prev_feat 512];
  * out: f32 [ck_output_size].  The first call (graph mode) captures the plan

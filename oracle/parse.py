@@ -36,8 +36,10 @@ def parse_mdn_single(raw, out_shape):
     return mu.reshape(shape), std.reshape(shape)
 
 
-def parse_mdn_mhp(raw, in_N, out_N, out_shape):
-    """`parse_mdn` with in_N > 1 hypotheses (parse_model_outputs.py:50-75)."""
+def parse_mdn_mhp(raw, in_N, out_N, out_shape, return_hypotheses=False):
+    """`parse_mdn` with in_N > 1 hypotheses (parse_model_outputs.py:50-75).
+    Returns (mu, std, weights) of the selections, plus (hypothesis mu,
+    hypothesis std) in the Parser's order when return_hypotheses."""
     raw = np.asarray(raw, np.float64)
     raw = raw.reshape(raw.shape[0], in_N, -1)
     n = (raw.shape[2] - out_N) // 2
@@ -60,4 +62,39 @@ def parse_mdn_mhp(raw, in_N, out_N, out_shape):
             mu_f[f, h] = mu[f, idx[0]]
             std_f[f, h] = std[f, idx[0]]
     shape = (raw.shape[0], out_N) + tuple(out_shape) if out_N > 1 else (raw.shape[0],) + tuple(out_shape)
+    if return_hypotheses:
+        hs = (raw.shape[0], in_N) + tuple(out_shape)
+        return mu_f.reshape(shape), std_f.reshape(shape), w, mu.reshape(hs), std.reshape(hs)
     return mu_f.reshape(shape), std_f.reshape(shape), w
+
+
+# The Parser's per-head calls (parse_model_outputs.py:95-115) with the
+# ModelConstants shapes they pass (constants.py:8-57).
+MDN_HEADS = {'pose': (6,), 'wide_from_device_euler': (3,), 'road_transform': (6,),
+             'lane_lines': (4, 33, 2), 'road_edges': (2, 33, 2), 'plan': (33, 15)}
+SIGMOID_HEADS = ('lane_lines_prob', 'meta', 'lead_prob')
+SOFTMAX_HEADS = {'desire_pred': (4, 8), 'desire_state': (8,)}
+LEAD_MDN_LEN = 2 * 3 * 6 * 4
+
+
+def parse_outputs(outs):
+    """Parser(ignore_missing=True).parse_outputs (parse_model_outputs.py:95-120)
+    on {name: raw array (1, len)}; heads the Parser does not name stay raw."""
+    outs = {k: np.asarray(v, np.float64) for k, v in outs.items()}
+    for name, shape in MDN_HEADS.items():
+        if name in outs:
+            outs[name], outs[name + '_stds'] = parse_mdn_single(outs[name], shape)
+    for name in SIGMOID_HEADS:
+        if name in outs:
+            outs[name] = sigmoid(outs[name])
+    for name, shape in SOFTMAX_HEADS.items():
+        if name in outs:
+            outs[name] = softmax(outs[name].reshape((outs[name].shape[0],) + shape), axis=-1)
+    if 'lead' in outs:
+        if outs['lead'].shape[1] == LEAD_MDN_LEN:       # is_mhp (parse_model_outputs.py:88-93)
+            outs['lead'], outs['lead_stds'] = parse_mdn_single(outs['lead'], (3, 6, 4))
+        else:
+            mu, std, w, hmu, hstd = parse_mdn_mhp(outs['lead'], 2, 3, (6, 4), return_hypotheses=True)
+            outs['lead'], outs['lead_stds'], outs['lead_weights'] = mu, std, w
+            outs['lead_hypotheses'], outs['lead_stds_hypotheses'] = hmu, hstd
+    return outs

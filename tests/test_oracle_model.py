@@ -149,3 +149,40 @@ def test_parse_mdn_mhp_selects_best_hypothesis():
     mu, std, w = PR.parse_mdn_mhp(raw.reshape(1, -1), 2, 1, (2,))
     np.testing.assert_allclose(mu.reshape(-1), [3, 4])
     assert w[0, 0, 0] > w[0, 1, 0]
+
+
+def test_parse_outputs_dict_closed_forms():
+    """The dict-level Parser restatement on hand-built raw heads."""
+    outs = {
+        'plan': np.concatenate([np.arange(495) / 100.0, np.full(495, 20.0)]).reshape(1, -1),
+        'lead_prob': np.zeros((1, 3)),
+        'desire_pred': np.zeros((1, 32)),
+        'lead': np.zeros((1, 144)),
+        'hidden_state': np.arange(4.0).reshape(1, 4),
+    }
+    p = PR.parse_outputs(outs)
+    assert p['plan'].shape == (1, 33, 15) and p['plan_stds'].shape == (1, 33, 15)
+    np.testing.assert_allclose(p['plan'].reshape(-1), np.arange(495) / 100.0)
+    np.testing.assert_allclose(p['plan_stds'], np.exp(11.0))           # safe_exp clips at 11
+    np.testing.assert_allclose(p['lead_prob'], 0.5)                    # sigmoid(0)
+    np.testing.assert_allclose(p['desire_pred'], 1 / 8)                # uniform groups of 8
+    assert p['desire_pred'].shape == (1, 4, 8)
+    assert p['lead'].shape == (1, 3, 6, 4)                             # 144 values: not multi-hypothesis
+    np.testing.assert_array_equal(p['hidden_state'], outs['hidden_state'])
+
+
+def test_parse_outputs_lead_mhp():
+    """2 hypotheses x (24 mu | 24 std | 3 weight logits): selection 0 goes to
+    hypothesis 1 (logit ln 3 vs 0: weights 1/4, 3/4), selections 1 and 2 to
+    hypothesis 0."""
+    raw = np.zeros((2, 51))
+    raw[0, :24], raw[1, :24] = 1.0, 2.0
+    raw[0, 24:48], raw[1, 24:48] = 0.0, np.log(2.0)
+    raw[0, 48:] = [0.0, 1.0, 1.0]
+    raw[1, 48:] = [np.log(3.0), 0.0, 0.0]
+    p = PR.parse_outputs({'lead': raw.reshape(1, -1)})
+    np.testing.assert_allclose(p['lead_weights'][0, :, 0], [0.25, 0.75])
+    np.testing.assert_allclose(p['lead'][0, 0], 2.0)
+    np.testing.assert_allclose(p['lead_stds'][0, 0], 2.0)
+    np.testing.assert_allclose(p['lead'][0, 1:], 1.0)
+    assert p['lead'].shape == (1, 3, 6, 4) and p['lead_hypotheses'].shape == (1, 2, 6, 4)
