@@ -44,8 +44,10 @@ def load_trace(path):
 def frames_from_trace(trace, plan):
     """Cut the dispatch sequence into frames that follow the plan in order:
     a frame starts at the plan's first kernel and every later entry must match
-    the next dispatch (a split-K reduce after a non-partials GEMM belongs to
-    the same entry).  Returns a list of per-entry durations (us) per frame."""
+    the next dispatch.  An entry may launch more than one kernel: a split-K
+    reduce after a non-partials GEMM, and further kernels of the same family
+    (e.g. the two passes of the column mean) when the next entry is of
+    another family, belong to it.  Returns per-entry durations (us) per frame."""
     first = _expect(plan[0]['kernel'])
     frames = []
     i = 0
@@ -54,14 +56,19 @@ def frames_from_trace(trace, plan):
             i += 1
             continue
         j, cur, ok = i, [], True
-        for e in plan:
-            if j >= len(trace) or _expect(e['kernel']) not in trace[j][0]:
+        for k, e in enumerate(plan):
+            tok = _expect(e['kernel'])
+            if j >= len(trace) or tok not in trace[j][0]:
                 ok = False
                 break
             us = trace[j][1]
             j += 1
             if '+splitk' in e['kernel'] and 'partials' not in e['kernel'] and j < len(trace) \
                     and 'splitk_reduce' in trace[j][0]:
+                us += trace[j][1]
+                j += 1
+            nxt = _expect(plan[k + 1]['kernel']) if k + 1 < len(plan) else None
+            while nxt != tok and j < len(trace) and tok in trace[j][0]:
                 us += trace[j][1]
                 j += 1
             cur.append(us)

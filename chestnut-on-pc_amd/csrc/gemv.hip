@@ -8,7 +8,13 @@
 //     2048-column step, and keeps its slice of x in registers for all rows;
 //   * every W read is one 16-byte load per lane, fully coalesced (a wave
 //     reads 1 KiB contiguous per instruction); RB rows are loaded before any
-//     arithmetic so each lane has RB*NSTEP loads in flight;
+//     arithmetic so each lane has RB*NSTEP loads in flight.  W is read once
+//     per frame and never again, so the loads are non-temporal (they do not
+//     displace x and the activations from the caches), which measures
+//     ~6% faster on the config-2 shape;
+//   * workgroups are small (one 4-row batch each for up to 4096 rows): three
+//     or more resident per CU keep more requests in flight than a few long
+//     workgroups would (3072 rows: 768 workgroups);
 //   * each lane accumulates its 8*NSTEP products in f32 (fixed order), the
 //     wave sums its lanes with DPP row exchanges + readlane, and the four
 //     wave partials are combined through LDS in wave order.
@@ -59,7 +65,7 @@ __global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(const half_t* __rest
       const half_t* wr = W + (long)r * ldw + t * 8;
 #pragma unroll
       for (int s = 0; s < NSTEP; ++s) {
-        if (cv[s]) w[i][s] = *reinterpret_cast<const half8_t*>(wr + s * GEMV_STEP_COLS);
+        if (cv[s]) w[i][s] = __builtin_nontemporal_load(reinterpret_cast<const half8_t*>(wr + s * GEMV_STEP_COLS));
         else w[i][s] = half8_t{};
       }
     }
@@ -110,7 +116,7 @@ void launch_gemv(const half_t* W, const float* x, const float* bias, float* y, i
              "gemv: W and x must be 16-byte aligned");
   CK_REQUIRE(act == GEMV_NONE || act == GEMV_GELU, "gemv: unknown activation");
   int rpw = rows_per_wg;
-  if (rpw <= 0) rpw = (rows + 511) / 512;           // ~2 workgroups per CU on 256 CUs
+  if (rpw <= 0) rpw = (rows + 1023) / 1024;         // >= 3 workgroups per CU up to 3072 rows
   rpw = ((rpw + GEMV_RB - 1) / GEMV_RB) * GEMV_RB;  // whole batches
   const int nstep = ceil_div(K, GEMV_STEP_COLS);
   switch (nstep) {

@@ -70,7 +70,9 @@ void launch_layernorm(const float* x, const float* g, const float* b, void* out,
 // the GEMM that produced x's update; ws[k] at ws + k*split_stride), then LN.
 void launch_add_layernorm(float* x, const float* ws, int nsplit, long split_stride, const float* rbias, const float* g,
                           const float* b, void* out, bool out_f16, int rows, int d, float eps, hipStream_t s);
-void launch_colmean(const float* x, float* out, int rows, int d, hipStream_t s);
+// out[n] = mean over rows of x[r][n]; part: colmean_workspace(rows, d) floats.
+size_t colmean_workspace(int rows, int d);
+void launch_colmean(const float* x, float* out, float* part, int rows, int d, hipStream_t s);
 void launch_gru_gate(const float* gi, const float* gh, const float* h_prev, float* h_out, float* h_out2,
                      int H, hipStream_t s);
 void launch_embed_init(const half_t* pos, const float* ctx, const float* bias, float* X, int T, int d,

@@ -55,10 +55,15 @@ __global__ __launch_bounds__(256) void layernorm_kernel(float* __restrict__ x, c
   }
 }
 
-// Wide rows (d >= 512): one 256-thread workgroup per row, EPT = d/256
-// elements per thread (coalesced: element tid + 256*i), so a row's x and
-// split-K partial loads are all independent and in flight together.  Row
-// sums: DPP wave sums, then the 4 wave sums combined through LDS in order.
+// Wide rows (d >= 512): one 256-thread workgroup per row.  Thread t owns the
+// VW-wide chunks t, t+256, ... (VW = 4, or 2 for d = 512), so every access is
+// a coalesced 8/16-byte vector.  All loads -- x, every split-K partial (up to
+// LN_MAXS), the bias, gamma and beta -- are issued before any arithmetic: one
+// memory round trip per row instead of one per partial.  Per element the
+// residual update is x + ((((ws0 + ws1) + ws2) + ...) + bias), in split
+// order.  Row sums: DPP wave sums, then the 4 wave sums through LDS in order.
+constexpr int LN_MAXS = 8;
+
 template <int EPT, bool OUT_F16, bool ADD>
 __global__ __launch_bounds__(256) void layernorm_row_kernel(float* __restrict__ x, const float* __restrict__ ws,
                                                             int nsplit, long split_stride,
@@ -66,52 +71,79 @@ __global__ __launch_bounds__(256) void layernorm_row_kernel(float* __restrict__ 
                                                             const float* __restrict__ g, const float* __restrict__ b,
                                                             void* __restrict__ out, float eps) {
   constexpr int D = EPT * 256;
+  constexpr int VW = EPT >= 4 ? 4 : EPT;
+  constexpr int NV = EPT / VW;
+  typedef float vec_t __attribute__((ext_vector_type(VW)));
+  typedef _Float16 hvec_t __attribute__((ext_vector_type(VW)));
   __shared__ float red[2][4];
   const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   float* xr = x + (long)row * D;
-  float v[EPT];
+  vec_t v[NV], gv[NV], bv[NV];
 #pragma unroll
-  for (int i = 0; i < EPT; ++i) v[i] = xr[tid + 256 * i];
+  for (int j = 0; j < NV; ++j) {
+    const int c = (j * 256 + tid) * VW;
+    v[j] = *reinterpret_cast<const vec_t*>(xr + c);
+    gv[j] = *reinterpret_cast<const vec_t*>(g + c);
+    bv[j] = *reinterpret_cast<const vec_t*>(b + c);
+  }
   if (ADD) {
-    float a[EPT];
-    const float* w = ws + (long)row * D + tid;
+    vec_t p[LN_MAXS][NV], rb[NV];
+    const float* w = ws + (long)row * D;
 #pragma unroll
-    for (int i = 0; i < EPT; ++i) a[i] = w[256 * i];
-    for (int k = 1; k < nsplit; ++k) {
+    for (int k = 0; k < LN_MAXS; ++k)
 #pragma unroll
-      for (int i = 0; i < EPT; ++i) a[i] += w[k * split_stride + 256 * i];
-    }
+      for (int j = 0; j < NV; ++j)
+        p[k][j] = k < nsplit ? *reinterpret_cast<const vec_t*>(w + k * split_stride + (j * 256 + tid) * VW) : vec_t{};
 #pragma unroll
-    for (int i = 0; i < EPT; ++i) {
-      if (rbias) a[i] += rbias[tid + 256 * i];
-      v[i] = v[i] + a[i];
-      xr[tid + 256 * i] = v[i];
+    for (int j = 0; j < NV; ++j)
+      rb[j] = rbias ? *reinterpret_cast<const vec_t*>(rbias + (j * 256 + tid) * VW) : vec_t{};
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      vec_t a = p[0][j];
+#pragma unroll
+      for (int k = 1; k < LN_MAXS; ++k)
+        if (k < nsplit) a += p[k][j];
+      if (rbias) a += rb[j];
+      v[j] = v[j] + a;
+      *reinterpret_cast<vec_t*>(xr + (j * 256 + tid) * VW) = v[j];
     }
   }
   float s = 0.f;
 #pragma unroll
-  for (int i = 0; i < EPT; ++i) s += v[i];
+  for (int j = 0; j < NV; ++j)
+#pragma unroll
+    for (int e = 0; e < VW; ++e) s += v[j][e];
   s = wave_sum(s);
   if (lane == 0) red[0][wave] = s;
   __syncthreads();
   const float mean = (((red[0][0] + red[0][1]) + red[0][2]) + red[0][3]) / (float)D;
   float q = 0.f;
 #pragma unroll
-  for (int i = 0; i < EPT; ++i) {
-    const float c = v[i] - mean;
-    q = fmaf(c, c, q);
-  }
+  for (int j = 0; j < NV; ++j)
+#pragma unroll
+    for (int e = 0; e < VW; ++e) {
+      const float c = v[j][e] - mean;
+      q = fmaf(c, c, q);
+    }
   q = wave_sum(q);
   if (lane == 0) red[1][wave] = q;
   __syncthreads();
   const float var = (((red[1][0] + red[1][1]) + red[1][2]) + red[1][3]) / (float)D;
   const float rstd = 1.0f / sqrtf(var + eps);
 #pragma unroll
-  for (int i = 0; i < EPT; ++i) {
-    const int c = tid + 256 * i;
-    const float y = (v[i] - mean) * rstd * g[c] + b[c];
-    if (OUT_F16) static_cast<half_t*>(out)[(long)row * D + c] = (half_t)y;
-    else static_cast<float*>(out)[(long)row * D + c] = y;
+  for (int j = 0; j < NV; ++j) {
+    const long c = (long)row * D + (j * 256 + tid) * VW;
+    vec_t y;
+#pragma unroll
+    for (int e = 0; e < VW; ++e) y[e] = (v[j][e] - mean) * rstd * gv[j][e] + bv[j][e];
+    if (OUT_F16) {
+      hvec_t h;
+#pragma unroll
+      for (int e = 0; e < VW; ++e) h[e] = (half_t)y[e];
+      *reinterpret_cast<hvec_t*>(static_cast<half_t*>(out) + c) = h;
+    } else {
+      *reinterpret_cast<vec_t*>(static_cast<float*>(out) + c) = y;
+    }
   }
 }
 
@@ -143,25 +175,41 @@ void ln_launch(float* x, const float* ws, int nsplit, long sstride, const float*
   CK_LAUNCHED("layernorm");
 }
 
-// out[n] = (1/rows) * sum_t x[t][n].  A workgroup owns 64 columns; its 8
-// waves sum interleaved row subsets (wave w: rows w, w+8, ...), and the 8
-// partial sums are combined in wave order through LDS (deterministic).
-__global__ __launch_bounds__(512) void colmean_kernel(const float* __restrict__ x, float* __restrict__ out, int rows,
-                                                      int d) {
-  __shared__ float part[8][64];
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int n = blockIdx.x * 64 + lane;
-  float s = 0.f;
-  if (n < d)
-    for (int t = w; t < rows; t += 8) s += x[(long)t * d + n];
-  part[w][lane] = s;
-  __syncthreads();
-  if (w == 0 && n < d) {
-    float a = part[0][lane];
+// Column mean (mean-pool over tokens) in two deterministic passes.  Pass 1:
+// one wave per block of 256 columns x 16 rows, float4 per lane, sums its 16
+// rows in row order into part[row block][column].  Pass 2 adds the row-block
+// partials of each column in block order and divides by the row count.  (A
+// single pass with a few long column walks leaves most CUs idle and each
+// lane waiting on one load after another.)
+constexpr int COLMEAN_ROWS = 16;
+
+__global__ __launch_bounds__(64) void colmean_part_kernel(const float* __restrict__ x, float* __restrict__ part,
+                                                         int rows, int d) {
+  const int c = blockIdx.x * 256 + threadIdx.x * 4;
+  const int r0 = blockIdx.y * COLMEAN_ROWS;
+  if (c >= d) return;
+  float4_t s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int k = 1; k < 8; ++k) a += part[k][lane];
-    out[n] = a / (float)rows;
+  for (int i = 0; i < COLMEAN_ROWS; ++i)
+    if (r0 + i < rows) s += *reinterpret_cast<const float4_t*>(x + (long)(r0 + i) * d + c);
+  *reinterpret_cast<float4_t*>(part + (long)blockIdx.y * d + c) = s;
+}
+
+__global__ __launch_bounds__(256) void colmean_final_kernel(const float* __restrict__ part, float* __restrict__ out,
+                                                           int nparts, int rows, int d) {
+  const int c = blockIdx.x * 256 + threadIdx.x;
+  if (c >= d) return;
+  // the partials are loaded in batches of 32 before they are added (in
+  // block order): one load latency per batch instead of one per partial
+  float s = 0.f;
+  for (int p0 = 0; p0 < nparts; p0 += 32) {
+    float v[32];
+#pragma unroll
+    for (int i = 0; i < 32; ++i) v[i] = p0 + i < nparts ? part[(long)(p0 + i) * d + c] : 0.f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) s += v[i];
   }
+  out[c] = s / (float)rows;
 }
 
 // GRU update (gate order r, z, n as rows [0,H), [H,2H), [2H,3H)):
@@ -215,7 +263,12 @@ void launch_layernorm(const float* x, const float* g, const float* b, void* out,
 void launch_add_layernorm(float* x, const float* ws, int nsplit, long split_stride, const float* rbias, const float* g,
                           const float* b, void* out, bool out_f16, int rows, int d, float eps, hipStream_t s) {
   CK_REQUIRE(x && g && b && out && rows > 0, "layernorm: bad arguments");
-  CK_REQUIRE(!ws || nsplit >= 1, "layernorm: residual partials need nsplit >= 1");
+  CK_REQUIRE(!ws || (nsplit >= 1 && nsplit <= LN_MAXS), "layernorm: residual partials need 1 <= nsplit <= 8");
+  if (d >= 512)
+    CK_REQUIRE(((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(ws) | reinterpret_cast<uintptr_t>(rbias) |
+                 reinterpret_cast<uintptr_t>(g) | reinterpret_cast<uintptr_t>(b) | reinterpret_cast<uintptr_t>(out)) &
+                15) == 0 && split_stride % 4 == 0,
+               "layernorm: wide rows need 16-byte aligned operands and a partial stride of whole vectors");
   switch (d) {
     case 128: ln_launch<2>(x, ws, nsplit, split_stride, rbias, g, b, out, out_f16, rows, eps, s); break;
     case 256: ln_launch<4>(x, ws, nsplit, split_stride, rbias, g, b, out, out_f16, rows, eps, s); break;
@@ -226,9 +279,16 @@ void launch_add_layernorm(float* x, const float* ws, int nsplit, long split_stri
   }
 }
 
-void launch_colmean(const float* x, float* out, int rows, int d, hipStream_t s) {
-  CK_REQUIRE(x && out && rows > 0 && d > 0, "colmean: bad arguments");
-  hipLaunchKernelGGL(colmean_kernel, dim3(ceil_div(d, 64)), dim3(512), 0, s, x, out, rows, d);
+size_t colmean_workspace(int rows, int d) { return (size_t)ceil_div(rows, COLMEAN_ROWS) * d; }
+
+void launch_colmean(const float* x, float* out, float* part, int rows, int d, hipStream_t s) {
+  CK_REQUIRE(x && out && part && rows > 0 && d > 0, "colmean: bad arguments");
+  CK_REQUIRE(d % 4 == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0 && (reinterpret_cast<uintptr_t>(part) & 15) == 0,
+             "colmean: d must be a multiple of 4, x and the workspace 16-byte aligned");
+  const int nparts = ceil_div(rows, COLMEAN_ROWS);
+  hipLaunchKernelGGL(colmean_part_kernel, dim3(ceil_div(d, 256), nparts), dim3(64), 0, s, x, part, rows, d);
+  CK_LAUNCHED("colmean");
+  hipLaunchKernelGGL(colmean_final_kernel, dim3(ceil_div(d, 256)), dim3(256), 0, s, part, out, nparts, rows, d);
   CK_LAUNCHED("colmean");
 }
 

@@ -10,12 +10,16 @@ PLAN = [
     {'name': 'blk0.o', 'kernel': 'gemm_partials+splitk4', 'flops': 8, 'bytes': 30},
     {'name': 'blk0.ln2', 'kernel': 'add_layernorm_f16', 'flops': 0, 'bytes': 40},
     {'name': 'blk1.o', 'kernel': 'gemm_partials+splitk4', 'flops': 8, 'bytes': 30},
+    {'name': 'final.pool', 'kernel': 'colmean', 'flops': 0, 'bytes': 8},
+    {'name': 'gru.ih', 'kernel': 'gemv', 'flops': 2, 'bytes': 8},
+    {'name': 'gru.hh', 'kernel': 'gemv', 'flops': 2, 'bytes': 8},
     {'name': 'tick', 'kernel': 'frame_tick', 'flops': 0, 'bytes': 4},
 ]
 FRAME = [('ck::policy_inputs_kernel(args)', 1.0), ('gemm_dma_kernel<64, 64, 5, 1, 2>', 2.0),
          ('splitk_reduce_kernel<2>', 0.5), ('gemm_dma_kernel<128, 128, 4, 2, 6>', 3.0),
          ('layernorm_row_kernel<8, true, true>', 4.0), ('gemm_dma_kernel<128, 128, 4, 2, 6>', 5.0),
-         ('frame_tick_kernel', 0.25)]
+         ('colmean_part_kernel', 1.5), ('colmean_final_kernel', 0.5), ('gemv_kernel<6>', 1.0),
+         ('gemv_kernel<1>', 2.0), ('frame_tick_kernel', 0.25)]
 
 
 def _trace_csv(path, seq):
@@ -34,11 +38,13 @@ def test_frames_follow_plan_order(tmp_path):
     _trace_csv(tmp_path / 't.csv', seq)
     frames = P.frames_from_trace(P.load_trace(tmp_path / 't.csv'), PLAN)
     assert len(frames) == 2
-    assert frames[0] == [1.0, 2.5, 3.0, 4.0, 5.0, 0.25]   # the reduce belongs to stem0.conv
+    # the reduce belongs to stem0.conv, both column-mean passes to final.pool,
+    # and the two GEMVs stay separate entries
+    assert frames[0] == [1.0, 2.5, 3.0, 4.0, 5.0, 2.0, 1.0, 2.0, 0.25]
 
 
 def test_frames_reject_mismatch(tmp_path):
-    bad = FRAME[:4] + [('attention_kernel', 1.0)] + FRAME[5:]
+    bad = FRAME[:4] + [('attention_kernel', 1.0)] + FRAME[5:]   # blk0.ln2 replaced
     _trace_csv(tmp_path / 't.csv', bad)
     assert P.frames_from_trace(P.load_trace(tmp_path / 't.csv'), PLAN) == []
 
