@@ -232,22 +232,40 @@ __global__ __launch_bounds__(256) void gemm_kernel(const GemmParams p) {
       }
 }
 
-// Sums split-K partials in split order, then applies the epilogue.
+// Sums split-K partials in split order, then applies the epilogue.  With
+// N % 4 == 0 a thread owns 4 consecutive outputs of one row (16-byte partial
+// loads); the partials of up to 8 splits are loaded before they are added.
 template <int EPI>
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(const GemmParams p) {
   const long MN = (long)p.M * p.N;
-  const long idx = (long)blockIdx.x * 256 + threadIdx.x;
+  const bool v4 = (p.N & 3) == 0;
+  const int per = v4 ? 4 : 1;
+  const long idx = ((long)blockIdx.x * 256 + threadIdx.x) * per;
   if (idx >= MN * p.batch) return;
   const int bz = (int)(idx / MN);
   const long r = idx - bz * MN;
   const int m = (int)(r / p.N), n = (int)(r - (long)m * p.N);
-  float v = 0.f;
-  for (int s = 0; s < p.split; ++s) v += p.ws[((long)s * p.batch + bz) * MN + r];
+  float v[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int s0 = 0; s0 < p.split; s0 += 8) {
+    float4_t part[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float* src = p.ws + ((long)(s0 + i) * p.batch + bz) * MN + r;
+      if (s0 + i >= p.split) part[i] = float4_t{0.f, 0.f, 0.f, 0.f};
+      else if (v4) part[i] = *reinterpret_cast<const float4_t*>(src);
+      else part[i] = float4_t{*src, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      if (s0 + i < p.split)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] += part[i][e];
+  }
   void* C = (EPI == EPI_F32 || EPI == EPI_F32_RESID)
                 ? static_cast<void*>(static_cast<float*>(p.C) + bz * p.sC)
                 : static_cast<void*>(static_cast<half_t*>(p.C) + bz * p.sC);
   const float* bias = p.bias ? p.bias + bz * p.sBias : nullptr;
-  epi_store<EPI>(p, C, bias, m, n, v);
+  for (int e = 0; e < per; ++e) epi_store<EPI>(p, C, bias, m, n + e, v[e]);
 }
 
 // ---------------------------------------------------------------------------
@@ -623,6 +641,39 @@ __global__ __launch_bounds__(256 * KG) void gemm_dma_kernel(const GemmParams p) 
       }
 }
 
+// B given as [K][N] (N contiguous, config 1's layout) is turned into the
+// [N][K] layout the LDS-DMA kernel streams: 64x64 tiles through LDS, 16-byte
+// global reads and writes.  The LDS pitch of 66 halves (33 words) keeps the
+// column reads of the write-out on distinct banks.
+__global__ __launch_bounds__(256) void transpose_kn_kernel(const half_t* __restrict__ src, long ld_src, long s_src,
+                                                           half_t* __restrict__ dst, long s_dst, int K, int N) {
+  __shared__ half_t t[64][66];
+  const int k0 = blockIdx.x * 64, n0 = blockIdx.y * 64;
+  src += blockIdx.z * s_src;
+  dst += blockIdx.z * s_dst;
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int r = tid / 8 + 32 * i, c = (tid % 8) * 8;   // k row r, n columns c..c+7
+    if (n0 + c < N) {
+      const half8_t v = *reinterpret_cast<const half8_t*>(src + (long)(k0 + r) * ld_src + n0 + c);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) t[r][c + e] = v[e];
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int r = tid / 8 + 32 * i, c = (tid % 8) * 8;   // n row r, k columns c..c+7
+    if (n0 + r < N) {
+      half8_t v;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = t[c + e][r];
+      *reinterpret_cast<half8_t*>(dst + (long)(n0 + r) * K + k0 + c) = v;
+    }
+  }
+}
+
 // LDS-DMA kernel configurations: KG = 2 (8 waves) where K allows, else KG = 1.
 template <int BM, int BN, int EPI>
 void launch_dma_tile(const GemmParams& p, bool kg2, hipStream_t s) {
@@ -642,12 +693,11 @@ void launch_tile(const GemmParams& p, hipStream_t s) {
   CK_LAUNCHED("gemm");
 }
 
-// tile codes 1-4: NT problems on the LDS-DMA kernel; 11-14 (and every [K][N]
-// problem) on the register-staged kernel.
 // tile codes (BM x BN): 1 128x128, 2 128x64, 3 64x128, 4 64x64.
 //   1-4: LDS-DMA kernel with two K-groups (8 waves) when K per split is a
-//        multiple of 128, else one group;  5-8: LDS-DMA, one group;
-//   11-14 (and every [K][N] problem): register-staged kernel.
+//        multiple of 128, else one group;  5-8: LDS-DMA, one group (a [K][N]
+//        B is first transposed into the workspace);
+//   11-14: register-staged kernel (a [K][N] B is transposed in registers).
 template <bool BKN, int EPI>
 void launch_epi(int tile, const GemmParams& p, hipStream_t s) {
   const int c = tile % 10;
@@ -671,7 +721,8 @@ void launch_epi(int tile, const GemmParams& p, hipStream_t s) {
 
 template <int EPI>
 void launch_reduce(const GemmParams& p, hipStream_t s) {
-  const long n = (long)p.M * p.N * p.batch;
+  const long n = (long)p.M * p.N * p.batch / ((p.N & 3) == 0 ? 4 : 1);
+  CK_REQUIRE((reinterpret_cast<uintptr_t>(p.ws) & 15) == 0, "gemm: split-K workspace must be 16-byte aligned");
   hipLaunchKernelGGL(splitk_reduce_kernel<EPI>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, p);
   CK_LAUNCHED("splitk_reduce");
 }
@@ -691,11 +742,11 @@ size_t gemm_plan(GemmDesc& d) {
     int bm = d.M <= 64 ? 64 : 128, bn = d.N <= 64 ? 64 : 128;
     const long t = (long)ceil_div(d.M, bm) * ceil_div(d.N, bn) * d.batch;
     if (t < 64 && d.K < 1024) bm = bn = 64;
-    if (d.b_kn) bn = 128;
     d.tile = bm == 128 ? (bn == 128 ? 1 : 2) : (bn == 128 ? 3 : 4);
   }
   CK_REQUIRE((d.tile >= 1 && d.tile <= 8) || (d.tile >= 11 && d.tile <= 14), "gemm: unknown tile code");
-  if (d.b_kn) CK_REQUIRE(d.tile == 11 || d.tile == 13 || d.tile == 1 || d.tile == 3, "gemm: [K][N] B needs a 128-wide N tile");
+  if (d.b_kn && d.tile > 10)
+    CK_REQUIRE(d.tile == 11 || d.tile == 13, "gemm: [K][N] B on the register-staged kernel needs a 128-wide N tile");
   const long tiles = (long)ceil_div(d.M, tile_bm(d.tile)) * ceil_div(d.N, tile_bn(d.tile)) * d.batch;
   if (d.split == 0) {
     // split K only while the grid stays within one wave of 256 CUs
@@ -704,7 +755,10 @@ size_t gemm_plan(GemmDesc& d) {
     d.split = s;
   }
   CK_REQUIRE(d.split >= 1 && d.K % (BK * d.split) == 0, "gemm: K must split into multiples of 64");
-  return (d.split > 1 || d.epi == EPI_PARTIALS) ? (size_t)d.split * d.batch * d.M * d.N : 0;
+  // workspace: split-K partials, then (a [K][N] B on the LDS-DMA kernel) B transposed to [N][K] f16
+  const size_t partials = (d.split > 1 || d.epi == EPI_PARTIALS) ? (size_t)d.split * d.batch * d.M * d.N : 0;
+  const size_t bt = (d.b_kn && d.tile < 10) ? ((size_t)d.batch * d.N * d.K + 1) / 2 : 0;
+  return partials + bt;
 }
 
 void launch_gemm(GemmDesc d, hipStream_t s) {
@@ -740,7 +794,7 @@ void launch_gemm(GemmDesc d, hipStream_t s) {
   {
     // the staged epilogue writes 16-byte chunks: 8 halves / 4 floats per chunk
     const auto al16 = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
-    bool v = !d.b_kn && d.N % 8 == 0;
+    bool v = !(d.b_kn && d.tile > 10) && d.N % 8 == 0;
     if (d.split > 1 || d.epi == EPI_PARTIALS) {
       v = v && al16(d.ws);
     } else {
@@ -759,8 +813,22 @@ void launch_gemm(GemmDesc d, hipStream_t s) {
     CK_REQUIRE(d.split == 1 && d.batch == 1 && d.tile < 10 && p.vec,
                "gemm: QKV fragment epilogue needs split 1, batch 1, an LDS-DMA tile and aligned outputs");
   }
-  if (d.b_kn) {
+  if (d.b_kn && d.tile > 10) {
     launch_epi<true, EPI_F32>(d.tile, p, s);
+    if (d.split > 1) launch_reduce<EPI_F32>(p, s);
+    return;
+  }
+  if (d.b_kn) {   // transpose B into the workspace tail, then the NT LDS-DMA kernel
+    const size_t partials = (d.split > 1) ? (size_t)d.split * d.batch * d.M * d.N : 0;
+    half_t* bt = reinterpret_cast<half_t*>(d.ws + partials);
+    CK_REQUIRE((reinterpret_cast<uintptr_t>(bt) & 15) == 0, "gemm: workspace must be 16-byte aligned");
+    hipLaunchKernelGGL(transpose_kn_kernel, dim3(d.K / 64, ceil_div(d.N, 64), d.batch), dim3(256), 0, s, d.B, d.ldb,
+                       d.sB, bt, (long)d.N * d.K, d.K, d.N);
+    CK_LAUNCHED("transpose_kn");
+    p.B = bt;
+    p.ldb = d.K;
+    p.sB = (long)d.N * d.K;
+    launch_epi<false, EPI_F32>(d.tile, p, s);
     if (d.split > 1) launch_reduce<EPI_F32>(p, s);
     return;
   }

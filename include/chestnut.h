@@ -150,8 +150,10 @@ int ck_gemv(const void* W, const float* x, const float* bias, float* y, int rows
 
 /* C f32 [M][N] = A f16 [M][K] (lda) * B, B f16 either [K][N] (b_kn = 1, ldb)
  * or [N][K] (b_kn = 0, ldb); optional bias f32 [N].  K % 64 == 0.
- * tile: 0 auto, 1 128x128, 2 128x64, 3 64x128, 4 64x64; split_k: 0 auto.
- * workspace: split_k * M * N floats when split_k > 1 (query with
+ * tile: 0 auto, 1 128x128, 2 128x64, 3 64x128, 4 64x64 (5-8: the same tiles
+ * with one K-group; 11, 13: the register-staged kernel); split_k: 0 auto.
+ * workspace: split_k * M * N floats when split_k > 1, plus, for a [K][N] B
+ * on tiles 1-8, N * K halves for B transposed to [N][K] (query with
  * ck_gemm_workspace, which also resolves auto tile/split).
  * Replaces: launch of the WMMA GEMM kernels r_6_2 / r_2_24 / r_12_32_4 /
  * r_48_32_4 (bench_r62.py:13-29, bench_r12.py, bench_r48.py). */

@@ -57,7 +57,8 @@ def test_gemm_planner_host_logic():
     t, s, nb = ctypes.c_int(0), ctypes.c_int(0), ctypes.c_size_t()
     # config 1: 1024 x 1024 output, K = 6144 -> 64 tiles of 128x128, split to fill 256 CUs
     _lib.call('ck_gemm_workspace', 1024, 1024, 6144, 1, ctypes.byref(t), ctypes.byref(s), ctypes.byref(nb))
-    assert t.value == 1 and s.value == 4 and nb.value == 4 * 1024 * 1024 * 4
+    # workspace: 4 split-K partial planes + B transposed to [N][K] f16
+    assert t.value == 1 and s.value == 4 and nb.value == 4 * 1024 * 1024 * 4 + 1024 * 6144 * 2
     t, s = ctypes.c_int(0), ctypes.c_int(0)
     # 1B MLP-up: 512 x 8192 -> 256 tiles, no split
     _lib.call('ck_gemm_workspace', 512, 8192, 2048, 0, ctypes.byref(t), ctypes.byref(s), ctypes.byref(nb))

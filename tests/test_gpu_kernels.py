@@ -153,6 +153,20 @@ def test_gemm_config1_full_size(gpu):
     _gemm_check(Ct, A, B)
 
 
+@pytest.mark.parametrize('tile', [0, 4, 5, 11, 13])
+@pytest.mark.parametrize('M,N,Kd,split', [(100, 200, 320, 1), (300, 136, 1024, 2)])
+def test_gemm_kn_paths(gpu, tile, M, N, Kd, split):
+    """[K][N] B: transposed into the workspace for the LDS-DMA tiles (0 auto,
+    4, 5), transposed in registers on the register-staged tiles (11, 13);
+    ragged M and N."""
+    from chestnut import kernels as K
+    rng = np.random.default_rng(M + N + tile)
+    A = rng.standard_normal((M, Kd)).astype(np.float16)
+    B = rng.standard_normal((Kd, N)).astype(np.float16)
+    C = host(K.gemm(dev(gpu, A), dev(gpu, B), b_kn=True, tile=tile, split_k=split))
+    _gemm_check(C, A, B)
+
+
 def test_gemm_matches_kchain_semantics(gpu):
     """Against the reference's FFMA-chain accumulation (16-wide K steps)."""
     from chestnut import kernels as K
@@ -166,9 +180,10 @@ def test_gemm_matches_kchain_semantics(gpu):
 
 
 @pytest.mark.parametrize('tile', [1, 2, 3, 4])
-# N % 8 == 0 takes the LDS-staged 16-byte epilogue, N = 100 the per-element one
+# N % 8 == 0 takes the LDS-staged 16-byte epilogue, N = 100 / 98 the per-element one
+# (98 with split 2: the scalar split-K reduce)
 @pytest.mark.parametrize('M,N,Kd,split', [(200, 136, 192, 1), (64, 64, 64, 1), (300, 520, 1024, 2), (33, 1000, 512, 4),
-                                          (72, 100, 128, 1)])
+                                          (72, 100, 128, 1), (64, 98, 512, 2)])
 def test_gemm_nt_tiles_tails(gpu, tile, M, N, Kd, split):
     from chestnut import kernels as K
     rng = np.random.default_rng(M * N + Kd + tile)
