@@ -464,6 +464,22 @@ __device__ __forceinline__ void store_staged(const GemmParams& p, const float16_
   }
 }
 
+// Issue the load instructions [lo, hi) of a K-step (A rows first, then B
+// rows); lo and hi are compile-time after unrolling, so the untaken ones vanish.
+template <int NIA, int NIB, int STAGE_A>
+__device__ __forceinline__ void dma_issue_range(const half_t* const* asrc, const half_t* const* bsrc, half_t* st,
+                                                int wave, int ko, int lo, int hi) {
+#pragma unroll
+  for (int i = 0; i < NIA; ++i)
+    if (i >= lo && i < hi)
+      __builtin_amdgcn_global_load_lds(asrc[i] + ko, (lds_ptr_t)(st + (wave * NIA + i) * 8 * BK), 16, 0, 0);
+#pragma unroll
+  for (int i = 0; i < NIB; ++i)
+    if (NIA + i >= lo && NIA + i < hi)
+      __builtin_amdgcn_global_load_lds(bsrc[i] + ko, (lds_ptr_t)(st + STAGE_A + (wave * NIB + i) * 8 * BK), 16, 0,
+                                       0);
+}
+
 // KG K-groups of 4 waves each (256*KG threads): group g consumes K-steps
 // g, g+KG, g+2KG, ... through its own S/KG stages of the ring, so KG=2 puts
 // 8 waves on a CU for one output tile (twice the loads in flight) without a
@@ -537,9 +553,14 @@ __global__ __launch_bounds__(256 * KG) void gemm_dma_kernel(const GemmParams p) 
     else if (P >= 2 && ahead >= 1) wait_vm_lgkm0<NI>();
     else wait_vm_lgkm0<0>();
     lds_barrier();
-    // refill the stage this group consumed at step t-1 (every wave passed the barrier)
-    if (t + P < nkg)
-      dma_issue<NIA, NIB, STAGE_A>(asrc, bsrc, lds + ((KG * (t + P) + grp) % S) * STAGE, w4, (KG * (t + P) + grp) * BK);
+    // refill the stage this group consumed at step t-1 (every wave passed the
+    // barrier).  The refill's NI load instructions are spread over the k-slices
+    // below, a few ahead of each slice's MFMAs: issued back to back they would
+    // hold the wave at the address unit for the whole step's worth of loads
+    // before its first MFMA.
+    const bool refill = t + P < nkg;
+    half_t* const rst = lds + ((KG * (t + P) + grp) % S) * STAGE;
+    const int rko = (KG * (t + P) + grp) * BK;
     const half_t* sa = lds + ((KG * t + grp) % S) * STAGE;
     const half_t* sb = sa + STAGE_A;
     // Two-deep software pipeline over the step's k-slices, each slice's
@@ -561,6 +582,7 @@ __global__ __launch_bounds__(256 * KG) void gemm_dma_kernel(const GemmParams p) 
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int kk = 0; kk < KS; ++kk) {
+      if (refill) dma_issue_range<NIA, NIB, STAGE_A>(asrc, bsrc, rst, w4, rko, kk * NI / KS, (kk + 1) * NI / KS);
 #pragma unroll
       for (int i = 0; i < FM; ++i)
 #pragma unroll
