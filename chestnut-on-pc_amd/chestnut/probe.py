@@ -22,7 +22,7 @@ baseline's (bench_r62.py:25-65).  Here:
             same way and compare every state tensor with post.npz.
 
     python -m chestnut.probe capture --spec big_driving_1b --entry blk0.up --out DIR
-    python -m chestnut.probe bench DIR [--lib PATH] [--gemm 5,2] [--reps 15]
+    python -m chestnut.probe bench DIR [--lib PATH] [--gemm 5,2] [--reps 15] [--ignore ws]
 
 Timings are per launch (HIP events around the single entry, no host
 launch overhead), so `med` is the kernel's own duration.
@@ -52,29 +52,41 @@ def _time_entry(eng, idx, pre, reps):
     return ts
 
 
-def compare(base, var):
+def compare(base, var, ignore=()):
     """bench_r62.py:57-65 statistics over every state tensor: bit-identical,
     number of differing elements, max abs / max rel difference over the
-    floating-point elements where the baseline is non-zero."""
+    floating-point elements where the baseline is non-zero.  `per_tensor`
+    holds (ndiff, maxabs, maxrel) of each differing tensor; tensors named in
+    `ignore` (scratch such as the split-K workspace "ws", which variants
+    with another split fill differently) are listed there but left out of
+    the totals."""
     ndiff, maxabs, maxrel = 0, 0.0, 0.0
     changed = []
+    per = {}
     for name, b in base.items():
         v = var[name]
         if b.shape != v.shape or b.dtype != v.dtype:
             raise ValueError(f'{name}: shape/dtype differ ({b.shape} {b.dtype} vs {v.shape} {v.dtype})')
         diff = b.view(np.uint8).reshape(-1, b.itemsize) != v.view(np.uint8).reshape(-1, b.itemsize)
         nd = int(diff.any(axis=1).sum())
-        if nd:
-            changed.append(name)
-        ndiff += nd
+        if not nd:
+            continue
+        ma, mr = 0.0, 0.0
         if b.dtype.kind == 'f':
             b64, v64 = b.astype(np.float64), v.astype(np.float64)
             nz = b64 != 0
             if nz.any():
                 d = np.abs(b64[nz] - v64[nz])
-                maxabs = max(maxabs, float(np.nanmax(d)))
-                maxrel = max(maxrel, float(np.nanmax(d / np.maximum(1e-30, np.abs(b64[nz])))))
-    return {'bit_identical': ndiff == 0, 'ndiff': ndiff, 'maxabs': maxabs, 'maxrel': maxrel, 'changed': changed}
+                ma = float(np.nanmax(d))
+                mr = float(np.nanmax(d / np.maximum(1e-30, np.abs(b64[nz]))))
+        per[name] = (nd, ma, mr)
+        if name in ignore:
+            continue
+        changed.append(name)
+        ndiff += nd
+        maxabs, maxrel = max(maxabs, ma), max(maxrel, mr)
+    return {'bit_identical': ndiff == 0, 'ndiff': ndiff, 'maxabs': maxabs, 'maxrel': maxrel, 'changed': changed,
+            'per_tensor': per}
 
 
 def fmt_times(ts):
@@ -118,7 +130,7 @@ def capture(spec_name, entry, out, frames=1, val=111, reps=15, gemm=None):
     return meta
 
 
-def bench(d, lib=None, gemm=None, reps=None):
+def bench(d, lib=None, gemm=None, reps=None, ignore=()):
     meta = json.load(open(os.path.join(d, 'meta.json')))
     sp = dict(meta['spec'])
     if gemm:
@@ -144,7 +156,7 @@ def bench(d, lib=None, gemm=None, reps=None):
     var = eng.snapshot()
     ts = _time_entry(eng, idx, pre, reps or meta['reps'])
     eng.close()
-    res = compare(base, {n: var[n] for n in base})
+    res = compare(base, {n: var[n] for n in base}, ignore)
     res['resized'] = resized
     res['variant_ms'] = ts
     res['baseline_ms'] = meta['baseline_ms']
@@ -167,6 +179,7 @@ def main(argv=None):
     b.add_argument('--lib', default=None)
     b.add_argument('--gemm', default=None, help='TILE,SPLIT for the entry in the variant')
     b.add_argument('--reps', type=int, default=None)
+    b.add_argument('--ignore', default='', help='comma-separated scratch tensors left out of the totals (e.g. ws)')
     a = ap.parse_args(argv)
     gemm = tuple(int(x) for x in a.gemm.split(',')) if a.gemm else None
     if a.cmd == 'capture':
@@ -175,12 +188,13 @@ def main(argv=None):
               f"captured to {a.out}", flush=True)
         print(f"baseline: {fmt_times(m['baseline_ms'])}", flush=True)
     else:
-        r = bench(a.dir, a.lib, gemm, a.reps)
+        r = bench(a.dir, a.lib, gemm, a.reps, tuple(x for x in a.ignore.split(',') if x))
         print(f"baseline: {fmt_times(r['baseline_ms'])}")
         print(f"variant : {fmt_times(r['variant_ms'])}  bit-identical={r['bit_identical']} ndiff={r['ndiff']} "
               f"maxabs={r['maxabs']:.3e} maxrel={r['maxrel']:.3e}", flush=True)
-        if r['changed']:
-            print(f"          differing tensors: {', '.join(r['changed'])}", flush=True)
+        for name, (nd, ma, mr) in r['per_tensor'].items():
+            print(f"          {name}: ndiff={nd} maxabs={ma:.3e} maxrel={mr:.3e}"
+                  f"{' (ignored)' if name not in r['changed'] else ''}", flush=True)
         if r['resized']:
             print(f"          not compared (size differs in the variant): {', '.join(r['resized'])}", flush=True)
 

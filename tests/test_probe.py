@@ -16,6 +16,11 @@ def test_compare_identical_and_diff():
     r = compare(base, var)
     assert not r['bit_identical'] and r['ndiff'] == 3 and r['changed'] == ['u', 'h']
     assert r['maxabs'] == 0.5 and r['maxrel'] == 0.25
+    assert r['per_tensor']['u'][0] == 2 and r['per_tensor']['h'][0] == 1
+    # scratch left out of the totals but still reported
+    r = compare(base, var, ignore=('u',))
+    assert r['changed'] == ['h'] and r['ndiff'] == 1 and 'u' in r['per_tensor']
+    assert r['maxrel'] < 1e-3
 
 
 def test_compare_negative_zero_is_a_bit_difference():
