@@ -518,6 +518,13 @@ void ck_engine::build_plan() {
     GemmDesc dn;
     dn.A = h16("u"); dn.lda = F; dn.B = h16(p + "down.w"); dn.ldb = F;
     dn.M = T; dn.N = d; dn.K = F; dn.epi = EPI_PARTIALS; dn.tile = 1; dn.split = s_dn;
+    // 256x128 tiles split 8 ways when that still fills 256 workgroups: each
+    // CU loads 3/4 of the bytes a 128x128 split-4 tile needs, for twice the
+    // partials (the LayerNorm after the block adds 8 instead of 4)
+    if (T % 256 == 0 && d % 128 == 0 && (F / 64) % 8 == 0 && F / 8 >= 128 && (T / 256) * (d / 128) * 8 >= 256) {
+      dn.tile = 9;
+      dn.split = 8;
+    }
     pend_split = add_gemm(b + "down", "gemm_partials", dn);
     pend_bias = f32(p + "down.b");
   }

@@ -480,25 +480,31 @@ __device__ __forceinline__ void dma_issue_range(const half_t* const* asrc, const
                                        0);
 }
 
-// KG K-groups of 4 waves each (256*KG threads): group g consumes K-steps
-// g, g+KG, g+2KG, ... through its own S/KG stages of the ring, so KG=2 puts
-// 8 waves on a CU for one output tile (twice the loads in flight) without a
-// global split-K reduce; the groups' accumulators are summed through LDS at
-// the end (group 0 + group 1, fixed order).
-template <int BM, int BN, int S, int KG, int EPI>
-__global__ __launch_bounds__(256 * KG) void gemm_dma_kernel(const GemmParams p) {
+// KG K-groups of NWG waves each (64*NWG*KG threads): group g consumes
+// K-steps g, g+KG, g+2KG, ... through its own S/KG stages of the ring, so
+// KG=2 puts 8 waves on a CU for one output tile (twice the loads in flight)
+// without a global split-K reduce; the groups' accumulators are summed
+// through LDS at the end (group 0 + group 1, fixed order).  A group's waves
+// form an (NWG/2) x 2 grid over the tile: NWG = 8 with a 256-row tile gives
+// every wave the same 64x64 sub-tile as NWG = 4 with 128 rows, while the CU
+// holds two waves per SIMD and each byte it loads feeds twice the MFMAs
+// along M.
+template <int BM, int BN, int S, int KG, int EPI, int NWG = 4>
+__global__ __launch_bounds__(64 * NWG * KG) void gemm_dma_kernel(const GemmParams p) {
   constexpr int STAGE_A = BM * BK, STAGE_B = BN * BK, STAGE = STAGE_A + STAGE_B;   // halves
   static_assert(S % KG == 0 && S / KG >= 2, "each K-group owns at least two ring stages");
+  static_assert(KG == 1 || NWG == 4, "K-groups are built from 4-wave groups");
   constexpr int P = S / KG - 1;   // steps a group keeps in flight while it computes
   __shared__ __attribute__((aligned(1024))) half_t lds[S * STAGE];
-  constexpr int WM = BM / 2, WN = BN / 2;
+  constexpr int WM = BM / (NWG / 2), WN = BN / 2;
   constexpr int FM = WM / 32, FN = WN / 32;
-  constexpr int NIA = BM / 32, NIB = BN / 32;   // load instructions per wave per step
+  constexpr int NIA = BM / (8 * NWG), NIB = BN / (8 * NWG);   // load instructions per wave per step
   constexpr int NI = NIA + NIB;
+  static_assert(NIA * 8 * NWG == BM && NIB * 8 * NWG == BN, "tile rows must split into whole load instructions");
   static_assert(KG == 1 || 4 * FM * FN * 16 * 64 * 4 <= S * STAGE * 2, "LDS too small for the group combine");
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int grp = wave >> 2, w4 = wave & 3;
+  const int grp = wave / NWG, w4 = wave % NWG;
   const int wm = w4 >> 1, wn = w4 & 1;
 
   const int total = p.Mt * p.Nt * p.split * p.batch;
@@ -627,7 +633,7 @@ __global__ __launch_bounds__(256 * KG) void gemm_dma_kernel(const GemmParams p) 
 
   if (p.vec) {
     constexpr int REGION = WM * (WN + 8) * 4;   // bytes per wave; the f32 staging is the largest
-    static_assert(4 * REGION <= S * STAGE * 2, "LDS ring too small for the staged epilogue");
+    static_assert(NWG * REGION <= S * STAGE * 2, "LDS ring too small for the staged epilogue");
     store_staged<WM, WN, FM, FN, EPI>(p, acc, reinterpret_cast<char*>(lds) + w4 * REGION, m0 + wm * WM,
                                       n0 + wn * WN, sp, bz, lane);
     return;
@@ -708,6 +714,14 @@ void launch_dma_tile(const GemmParams& p, bool kg2, hipStream_t s) {
   CK_LAUNCHED("gemm_dma");
 }
 
+// 256x128 tile: 8 waves of 64x64, one K-group, 3-stage ring (3 x 48 KB).
+template <int EPI>
+void launch_dma_tile8(const GemmParams& p, hipStream_t s) {
+  const int grid = p.Mt * p.Nt * p.split * p.batch;
+  hipLaunchKernelGGL((gemm_dma_kernel<256, 128, 3, 1, EPI, 8>), dim3(grid), dim3(512), 0, s, p);
+  CK_LAUNCHED("gemm_dma");
+}
+
 template <int BM, int BN, bool BKN, int EPI>
 void launch_tile(const GemmParams& p, hipStream_t s) {
   const int grid = p.Mt * p.Nt * p.split * p.batch;
@@ -719,10 +733,15 @@ void launch_tile(const GemmParams& p, hipStream_t s) {
 //   1-4: LDS-DMA kernel with two K-groups (8 waves) when K per split is a
 //        multiple of 128, else one group;  5-8: LDS-DMA, one group (a [K][N]
 //        B is first transposed into the workspace);
+//   9: 256x128 on the LDS-DMA kernel with 8 waves in one K-group;
 //   11-14: register-staged kernel (a [K][N] B is transposed in registers).
 template <bool BKN, int EPI>
 void launch_epi(int tile, const GemmParams& p, hipStream_t s) {
   const int c = tile % 10;
+  if (!BKN && tile == 9) {
+    launch_dma_tile8<EPI>(p, s);
+    return;
+  }
   if (!BKN && tile < 10) {
     const bool kg2 = c <= 4 && p.kps % (2 * BK) == 0;
     switch (c > 4 ? c - 4 : c) {
@@ -750,8 +769,8 @@ void launch_reduce(const GemmParams& p, hipStream_t s) {
 }
 
 int tile_base(int tile) { const int c = tile % 10; return c > 4 ? c - 4 : c; }
-int tile_bm(int tile) { return (tile_base(tile) == 1 || tile_base(tile) == 2) ? 128 : 64; }
-int tile_bn(int tile) { return (tile_base(tile) == 1 || tile_base(tile) == 3) ? 128 : 64; }
+int tile_bm(int tile) { return tile == 9 ? 256 : (tile_base(tile) == 1 || tile_base(tile) == 2) ? 128 : 64; }
+int tile_bn(int tile) { return tile == 9 ? 128 : (tile_base(tile) == 1 || tile_base(tile) == 3) ? 128 : 64; }
 
 }  // namespace
 
@@ -766,7 +785,7 @@ size_t gemm_plan(GemmDesc& d) {
     if (t < 64) bm = bn = 64;
     d.tile = bm == 128 ? (bn == 128 ? 1 : 2) : (bn == 128 ? 3 : 4);
   }
-  CK_REQUIRE((d.tile >= 1 && d.tile <= 8) || (d.tile >= 11 && d.tile <= 14), "gemm: unknown tile code");
+  CK_REQUIRE((d.tile >= 1 && d.tile <= 9) || (d.tile >= 11 && d.tile <= 14), "gemm: unknown tile code");
   if (d.b_kn && d.tile > 10)
     CK_REQUIRE(d.tile == 11 || d.tile == 13, "gemm: [K][N] B on the register-staged kernel needs a 128-wide N tile");
   const long tiles = (long)ceil_div(d.M, tile_bm(d.tile)) * ceil_div(d.N, tile_bn(d.tile)) * d.batch;

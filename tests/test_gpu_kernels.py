@@ -179,7 +179,7 @@ def test_gemm_matches_kchain_semantics(gpu):
     assert np.all(np.abs(C - chain) <= (1024 + 64 + 32) * U * scale)
 
 
-@pytest.mark.parametrize('tile', [1, 2, 3, 4])
+@pytest.mark.parametrize('tile', [1, 2, 3, 4, 9])
 # N % 8 == 0 takes the LDS-staged 16-byte epilogue, N = 100 / 98 the per-element one
 # (98 with split 2: the scalar split-K reduce)
 @pytest.mark.parametrize('M,N,Kd,split', [(200, 136, 192, 1), (64, 64, 64, 1), (300, 520, 1024, 2), (33, 1000, 512, 4),
