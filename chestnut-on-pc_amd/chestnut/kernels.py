@@ -136,3 +136,18 @@ def layernorm(x, g, b, eps=1e-5, out_f16=True):
     out = torch.empty(rows, d, dtype=torch.float16 if out_f16 else torch.float32, device=x.device)
     call('ck_layernorm', _ptr(x), _ptr(g), _ptr(b), _ptr(out), 1 if out_f16 else 0, rows, d, eps, _stream())
     return out
+
+
+def warp_nv12(frame, big_frame, tfm, big_tfm, cam_w, cam_h, stride, y_height, model_w=512, model_h=256):
+    """NV12 frames (u8 device buffers) + f32 [3,3] inverse transforms ->
+    u8 [2, 6, model_h/2, model_w/2] (the engine's `warped`)."""
+    for t, n in ((frame, 'frame'), (big_frame, 'big_frame')):
+        _need(t, torch.uint8, n)
+    for t, n in ((tfm, 'tfm'), (big_tfm, 'big_tfm')):
+        _need(t, torch.float32, n)
+    if frame.numel() != big_frame.numel() or tfm.numel() != 9 or big_tfm.numel() != 9:
+        raise ValueError('frames must have the same size and transforms 9 floats')
+    out = torch.empty(2, 6, model_h // 2, model_w // 2, dtype=torch.uint8, device=frame.device)
+    call('ck_warp_nv12', _ptr(frame), _ptr(big_frame), frame.numel(), _ptr(tfm), _ptr(big_tfm), cam_w, cam_h, stride,
+         y_height, model_w, model_h, _ptr(out), _stream())
+    return out

@@ -364,6 +364,15 @@ int ck_img_gather(const void* img, int A, int B, int lanes, int elem_bytes, cons
   CK_API_END
 }
 
+int ck_warp_nv12(const uint8_t* frame, const uint8_t* big_frame, size_t frame_bytes, const float* tfm,
+                 const float* big_tfm, int cam_w, int cam_h, int stride, int y_height, int model_w, int model_h,
+                 uint8_t* out, void* stream) {
+  CK_API_BEGIN
+  launch_warp_nv12(frame, big_frame, frame_bytes, tfm, big_tfm, cam_w, cam_h, stride, y_height, model_w, model_h, out,
+                   as_stream(stream));
+  CK_API_END
+}
+
 int ck_attention(const void* qk, const void* vt, void* out, int T, int n_heads, int head_dim, void* stream) {
   CK_API_BEGIN
   launch_attention(static_cast<const half_t*>(qk), static_cast<const half_t*>(vt), static_cast<half_t*>(out), T,

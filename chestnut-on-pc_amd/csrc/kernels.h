@@ -93,6 +93,14 @@ struct DecodeHead {
 // One workgroup per head; heads_dev is a device copy of the table.
 void launch_decode(const float* raw, float* decoded, const DecodeHead* heads_dev, int n_heads, hipStream_t s);
 
+// ---- NV12 perspective warp -> `warped` (compile_modeld.py:53-118, 181-193) ----
+// frame, big_frame: NV12 (Y plane of y_height rows, then the interleaved UV
+// plane), rows of `stride` bytes, frame_bytes each; tfm, big_tfm: device f32
+// [3][3] inverse transforms; out u8 [2][6][model_h/2][model_w/2].
+void launch_warp_nv12(const uint8_t* frame, const uint8_t* big_frame, size_t frame_bytes, const float* tfm,
+                      const float* big_tfm, int cam_w, int cam_h, int stride, int y_height, int model_w, int model_h,
+                      uint8_t* out, hipStream_t s);
+
 // ---- frame inputs, packing, image2d ------------------------------------------
 struct QueueDims {
   int img_h, img_w;          // 128, 256

@@ -168,6 +168,19 @@ int ck_gemm(const void* A, const void* B, float* C, const float* bias, int M, in
 int ck_gemm_epi(const void* A, const void* B, void* C, const float* bias, int M, int N, int K, long lda, long ldb,
                 long ldc, int epi, int tile, int split_k, void* workspace, size_t ws_bytes, void* stream);
 
+/* NV12 camera frames -> the 6-channel model input `warped`: perspective
+ * warp with nearest-neighbour sampling (f32 coordinates, round half to
+ * even, clipped to the edge), Y at model_w x model_h, U and V from the
+ * interleaved UV plane at half resolution, packed as frames_to_tensor does.
+ * frame, big_frame: device NV12 buffers of frame_bytes (Y plane: y_height
+ * rows of stride bytes, then the UV plane); tfm, big_tfm: device f32 [3][3]
+ * inverse transforms; out: device u8 [2][6][model_h/2][model_w/2].
+ * Replaces: make_warp / frame_prepare_tinygrad / warp_perspective_tinygrad
+ * (compile_modeld.py:53-118, 181-193). */
+int ck_warp_nv12(const uint8_t* frame, const uint8_t* big_frame, size_t frame_bytes, const float* tfm,
+                 const float* big_tfm, int cam_w, int cam_h, int stride, int y_height, int model_w, int model_h,
+                 uint8_t* out, void* stream);
+
 /* n_tiles WMMA uops ((16,16,16), half, 'AMD', 32): per tile u16 fragA[32][8],
  * fragB[32][8], f32 fragC[32][8] -> f32 fragD[32][8], RDNA4 lane layout.
  * Replaces: _wm_emit's WMMA lowering (run_pinned2.py:119-266) and the
