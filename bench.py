@@ -67,8 +67,9 @@ def kernel_table(eng, reps=3):
 
 def micro(torch):
     """BASELINE configs 1 and 2 as single kernels, cold-cache (rotating copies
-    larger than the 256 MB Infinity Cache), HIP events on torch's stream."""
-    from chestnut import kernels as K
+    larger than the 256 MB Infinity Cache), and the NV12 warp of a road-camera
+    frame pair; HIP events on torch's stream."""
+    from chestnut import kernels as K, spec as S
     res = {}
     n_copies = 5
     W = [torch.randn(3072, 12288, device='cuda', dtype=torch.float16) * 0.02 for _ in range(n_copies)]
@@ -111,6 +112,24 @@ def micro(torch):
     res['gemm_config1'] = {'shape': [1024, 6144, 1024], 'us': round(us, 2), 'tflops': round(fl / us / 1e6, 1),
                            'frac_mfma': round(fl / us / 1e6 / PEAK_F16_TFLOPS, 4), 'tile': tile, 'split_k': split,
                            'copies': n_copies}
+    # NV12 road-camera warp of both frames (the step before `warped`)
+    cam = S.ROAD_CAMERA
+    nb = S.nv12_bytes(cam)
+    fr = [torch.randint(0, 256, (nb,), dtype=torch.uint8, device='cuda') for _ in range(2)]
+    tfm = torch.tensor([[3.7, -0.05, 10.0], [0.05, 3.7, 120.0], [1e-5, 2e-5, 1.0]], device='cuda')
+    wout = torch.empty(2, 6, 128, 256, dtype=torch.uint8, device='cuda')
+    geo = dict(cam_w=cam['width'], cam_h=cam['height'], stride=cam['stride'], y_height=cam['y_height'])
+    K.warp_nv12(fr[0], fr[1], tfm, tfm, out=wout, **geo)
+    reps = 200
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(reps):
+        K.warp_nv12(fr[0], fr[1], tfm, tfm, out=wout, **geo)
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / reps
+    res['warp_nv12'] = {'camera': [cam['width'], cam['height']], 'model': [512, 256], 'us': round(us, 2),
+                        'out_bytes': wout.numel()}
     return res
 
 
@@ -179,6 +198,7 @@ def main():
     from chestnut import Engine, spec as S
 
     sp = S.get_spec(a.spec)
+    sp.setdefault('camera', S.ROAD_CAMERA)     # accepts raw NV12 frames as well (run_frame_nv12)
     t0 = time.perf_counter()
     weights = S.make_weights(sp)
     log(f'[bench] {sp["name"]}: {S.param_count(sp) / 1e6:.1f}M params generated in {time.perf_counter() - t0:.1f}s')
@@ -225,6 +245,16 @@ def main():
         o = eng.run_frame(warped, pk)
         pk[12:] = o[eng.out_slices['hidden_state']]
     host_fps = n_host / (time.perf_counter() - t0)
+    # modeld's flow: two NV12 road-camera frames (2 x 3.7 MB over PCIe) warped on device
+    nb = S.nv12_bytes(sp['camera'])
+    frames = [rng.integers(0, 256, nb, dtype=np.uint8) for _ in range(2)]
+    tfm = np.array([[3.7, -0.05, 10.0], [0.05, 3.7, 120.0], [1e-5, 2e-5, 1.0]], np.float32)
+    eng.run_frame_nv12(frames[0], frames[1], tfm, tfm, packed)
+    t0 = time.perf_counter()
+    for _ in range(n_host):
+        o = eng.run_frame_nv12(frames[0], frames[1], tfm, tfm, pk)
+        pk[12:] = o[eng.out_slices['hidden_state']]
+    nv12_fps = n_host / (time.perf_counter() - t0)
 
     # device-resident frames: inputs in HBM, back-to-back graph launches
     eng.write('warped', warped)
@@ -247,7 +277,7 @@ def main():
     gpu_ms = e0.elapsed_time(e1)
     fps = a.steps / wall
     log(f'[bench] {a.steps} frames: wall {wall * 1e3:.2f} ms ({fps:.1f} fps), events {gpu_ms:.2f} ms, '
-        f'host-inclusive {host_fps:.1f} fps')
+        f'host-inclusive {host_fps:.1f} fps, NV12 host-inclusive {nv12_fps:.1f} fps')
 
     rows, plan, fams = kernel_table(eng)
     for r in rows[:12]:
@@ -279,7 +309,8 @@ def main():
                                    f'MLP {sp["d_ff"]}, {sp["stem"][-1]} tokens -> temporal GEMV, GRU, heads)',
                        'params': S.param_count(sp), 'graph_nodes': eng.graph_nodes(), 'launches': len(plan),
                        'event_ms_per_step': round(gpu_ms / a.steps, 4),
-                       'host_inclusive_fps': round(host_fps, 2)},
+                       'host_inclusive_fps': round(host_fps, 2),
+                       'nv12_host_inclusive_fps': round(nv12_fps, 2)},
             'roofline': roof, 'kernels': rows}
     if not a.no_micro:
         line['micro'] = micro(torch)

@@ -29,6 +29,7 @@ _SIGS = {
     'ck_output_size': (c_int, [c_void_p, P(c_int)]),
     'ck_output_slices': (c_int, [c_void_p, ctypes.c_char_p, c_size_t]),
     'ck_run_frame': (c_int, [c_void_p, c_void_p, c_void_p, c_void_p]),
+    'ck_run_frame_nv12': (c_int, [c_void_p, c_void_p, c_void_p, c_size_t, c_void_p, c_void_p, c_void_p, c_void_p]),
     'ck_set_graph': (c_int, [c_void_p, c_int]),
     'ck_graph_nodes': (c_int, [c_void_p, P(c_size_t)]),
     'ck_reset': (c_int, [c_void_p]),

@@ -123,6 +123,31 @@ class Engine:
         call('ck_run_frame', self._h, w.ctypes.data, p.ctypes.data, out.ctypes.data)
         return out
 
+    def run_frame_nv12(self, frame, big_frame, tfm, big_tfm, packed):
+        """One step of modeld's flow (compile_modeld.py:181-221): two NV12
+        frames (flat uint8, the spec's "camera" geometry) and their f32 3x3
+        inverse transforms are warped on device, then the frame runs as in
+        run_frame.  Returns the flat f32 output vector."""
+        cam = self.spec.get('camera')
+        if not cam:
+            raise ValueError('run_frame_nv12 needs a spec with a "camera" object')
+        nb = _spec.nv12_bytes(cam)
+        f = np.ascontiguousarray(frame, dtype=np.uint8).reshape(-1)
+        bf = np.ascontiguousarray(big_frame, dtype=np.uint8).reshape(-1)
+        if f.size != nb or bf.size != nb:
+            raise ValueError(f'frames must be {nb} bytes of NV12, got {f.size} and {bf.size}')
+        t = np.ascontiguousarray(tfm, dtype=np.float32)
+        bt = np.ascontiguousarray(big_tfm, dtype=np.float32)
+        if t.size != 9 or bt.size != 9:
+            raise ValueError('transforms must be 3x3')
+        p = np.ascontiguousarray(packed, dtype=np.float32)
+        if p.shape != self.PACKED.shape:
+            raise ValueError(f'packed must be f32 {self.PACKED.shape}, got {p.shape}')
+        out = np.empty(self.n_out, np.float32)
+        call('ck_run_frame_nv12', self._h, f.ctypes.data, bf.ctypes.data, nb, t.ctypes.data, bt.ctypes.data,
+             p.ctypes.data, out.ctypes.data)
+        return out
+
     def make_warped(self, val=128):
         """Constant frame pair (run_pinned2.py:1388-1389)."""
         s = self.spec

@@ -138,7 +138,7 @@ def layernorm(x, g, b, eps=1e-5, out_f16=True):
     return out
 
 
-def warp_nv12(frame, big_frame, tfm, big_tfm, cam_w, cam_h, stride, y_height, model_w=512, model_h=256):
+def warp_nv12(frame, big_frame, tfm, big_tfm, cam_w, cam_h, stride, y_height, model_w=512, model_h=256, out=None):
     """NV12 frames (u8 device buffers) + f32 [3,3] inverse transforms ->
     u8 [2, 6, model_h/2, model_w/2] (the engine's `warped`)."""
     for t, n in ((frame, 'frame'), (big_frame, 'big_frame')):
@@ -147,7 +147,13 @@ def warp_nv12(frame, big_frame, tfm, big_tfm, cam_w, cam_h, stride, y_height, mo
         _need(t, torch.float32, n)
     if frame.numel() != big_frame.numel() or tfm.numel() != 9 or big_tfm.numel() != 9:
         raise ValueError('frames must have the same size and transforms 9 floats')
-    out = torch.empty(2, 6, model_h // 2, model_w // 2, dtype=torch.uint8, device=frame.device)
+    shape = (2, 6, model_h // 2, model_w // 2)
+    if out is None:
+        out = torch.empty(shape, dtype=torch.uint8, device=frame.device)
+    else:
+        _need(out, torch.uint8, 'out')
+        if tuple(out.shape) != shape:
+            raise ValueError(f'out must be uint8 {shape}')
     call('ck_warp_nv12', _ptr(frame), _ptr(big_frame), frame.numel(), _ptr(tfm), _ptr(big_tfm), cam_w, cam_h, stride,
          y_height, model_w, model_h, _ptr(out), _stream())
     return out

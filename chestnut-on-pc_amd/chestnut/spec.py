@@ -49,6 +49,19 @@ SPECS = {
 }
 
 
+# NV12 geometry of a road-camera frame (1928x1208, rows padded to 2048 bytes,
+# Y plane padded to 1216 rows), as openpilot's camerad hands it to modeld
+# (compile_modeld.py:16-31).  A spec with a "camera" object accepts raw NV12
+# frames (Engine.run_frame_nv12) and warps them on device.
+ROAD_CAMERA = dict(width=1928, height=1208, stride=2048, y_height=1216)
+
+
+def nv12_bytes(camera):
+    """Bytes of one NV12 frame: the padded Y plane and the half-height
+    interleaved UV rows (compile_modeld.py:97-104)."""
+    return camera['stride'] * camera['y_height'] + (camera['height'] // 2) * camera['stride']
+
+
 def get_spec(name_or_spec):
     if isinstance(name_or_spec, dict):
         return dict(name_or_spec)

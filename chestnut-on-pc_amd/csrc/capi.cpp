@@ -159,6 +159,16 @@ int ck_run_frame(ck_engine* e, const uint8_t* warped, const float* packed, float
   CK_API_END
 }
 
+int ck_run_frame_nv12(ck_engine* e, const uint8_t* frame, const uint8_t* big_frame, size_t frame_bytes,
+                      const float* tfm, const float* big_tfm, const float* packed, float* out) {
+  CK_API_BEGIN
+  CK_REQUIRE(e && frame && big_frame && tfm && big_tfm && packed && out, "null argument");
+  CK_REQUIRE(frame_bytes == e->nv12_bytes, "run_frame_nv12: frame_bytes " + std::to_string(frame_bytes) +
+                                               " != the camera's NV12 size " + std::to_string(e->nv12_bytes));
+  e->run_frame_nv12(frame, big_frame, tfm, big_tfm, packed, out);
+  CK_API_END
+}
+
 int ck_set_graph(ck_engine* e, int on) {
   CK_API_BEGIN
   CK_REQUIRE(e, "null engine");

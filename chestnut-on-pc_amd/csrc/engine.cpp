@@ -69,6 +69,16 @@ Spec parse_spec(const std::string& json) {
       s.outputs.emplace_back(e.arr[0].str, (int)e.arr[1].num);
     }
   }
+  if (const JVal* cam = o.get("camera")) {
+    CK_REQUIRE(cam->kind == JVal::OBJ, "spec: camera must be an object {width, height, stride, y_height}");
+    s.cam_w = jint(*cam, "width", 0, true);
+    s.cam_h = jint(*cam, "height", 0, true);
+    s.cam_stride = jint(*cam, "stride", 0, true);
+    s.cam_y_height = jint(*cam, "y_height", 0, true);
+    CK_REQUIRE(s.cam_w > 0 && s.cam_h > 0 && s.cam_w % 2 == 0 && s.cam_h % 2 == 0 && s.cam_stride >= s.cam_w &&
+                   s.cam_y_height >= s.cam_h,
+               "spec: camera needs an even width and height, stride >= width, y_height >= height");
+  }
   if (const JVal* gc = o.get("gemm_config")) {
     CK_REQUIRE(gc->kind == JVal::OBJ, "spec: gemm_config must be an object {entry: [tile, split]}");
     for (const auto& kv : gc->obj) {
@@ -112,6 +122,13 @@ ck_engine::ck_engine(const std::string& spec_json) : sp(parse_spec(spec_json)) {
   CK_HIP(hipHostMalloc((void**)&h_warped, warped_bytes, hipHostMallocDefault));
   CK_HIP(hipHostMalloc((void**)&h_packed, packed_len * sizeof(float), hipHostMallocDefault));
   CK_HIP(hipHostMalloc((void**)&h_out, n_out * sizeof(float), hipHostMallocDefault));
+  if (sp.cam_w) {
+    nv12_bytes = (size_t)sp.cam_stride * sp.cam_y_height + (size_t)(sp.cam_h / 2) * sp.cam_stride;
+    add_tensor("nv12", 2 * nv12_bytes, DT_U8, false);
+    add_tensor("tfm", 18 * sizeof(float), DT_F32, false);
+    CK_HIP(hipHostMalloc((void**)&h_nv12, 2 * nv12_bytes, hipHostMallocDefault));
+    CK_HIP(hipHostMalloc((void**)&h_tfm, 18 * sizeof(float), hipHostMallocDefault));
+  }
   reset_state();
 }
 
@@ -124,6 +141,8 @@ ck_engine::~ck_engine() {
   if (h_warped) (void)hipHostFree(h_warped);
   if (h_packed) (void)hipHostFree(h_packed);
   if (h_out) (void)hipHostFree(h_out);
+  if (h_nv12) (void)hipHostFree(h_nv12);
+  if (h_tfm) (void)hipHostFree(h_tfm);
   if (stream) (void)hipStreamDestroy(stream);
 }
 
@@ -623,6 +642,31 @@ void ck_engine::run_frame(const uint8_t* warped, const float* packed, float* out
   std::memcpy(h_packed, packed, packed_len * sizeof(float));
   CK_HIP(hipMemcpyAsync(ptr("warped"), h_warped, warped_bytes, hipMemcpyHostToDevice, stream));
   CK_HIP(hipMemcpyAsync(ptr("packed"), h_packed, packed_len * sizeof(float), hipMemcpyHostToDevice, stream));
+  frame_launch();
+  CK_HIP(hipMemcpyAsync(h_out, ptr("out"), n_out * sizeof(float), hipMemcpyDeviceToHost, stream));
+  CK_HIP(hipStreamSynchronize(stream));
+  std::memcpy(out, h_out, n_out * sizeof(float));
+}
+
+// The openpilot per-frame flow: two NV12 camera frames and their inverse
+// transforms are staged, warped into `warped` on device (warp.hip), then the
+// frame plan runs as in run_frame.  The warp is one launch ahead of the
+// frame's graph.
+void ck_engine::run_frame_nv12(const uint8_t* frame, const uint8_t* big_frame, const float* tfm, const float* big_tfm,
+                               const float* packed, float* out) {
+  CK_REQUIRE(nv12_bytes, "run_frame_nv12: the spec has no camera");
+  std::memcpy(h_nv12, frame, nv12_bytes);
+  std::memcpy(h_nv12 + nv12_bytes, big_frame, nv12_bytes);
+  std::memcpy(h_tfm, tfm, 9 * sizeof(float));
+  std::memcpy(h_tfm + 9, big_tfm, 9 * sizeof(float));
+  std::memcpy(h_packed, packed, packed_len * sizeof(float));
+  uint8_t* nv = static_cast<uint8_t*>(ptr("nv12"));
+  float* tf = static_cast<float*>(ptr("tfm"));
+  CK_HIP(hipMemcpyAsync(nv, h_nv12, 2 * nv12_bytes, hipMemcpyHostToDevice, stream));
+  CK_HIP(hipMemcpyAsync(tf, h_tfm, 18 * sizeof(float), hipMemcpyHostToDevice, stream));
+  CK_HIP(hipMemcpyAsync(ptr("packed"), h_packed, packed_len * sizeof(float), hipMemcpyHostToDevice, stream));
+  launch_warp_nv12(nv, nv + nv12_bytes, nv12_bytes, tf, tf + 9, sp.cam_w, sp.cam_h, sp.cam_stride, sp.cam_y_height,
+                   2 * sp.img_w, 2 * sp.img_h, static_cast<uint8_t*>(ptr("warped")), stream);
   frame_launch();
   CK_HIP(hipMemcpyAsync(h_out, ptr("out"), n_out * sizeof(float), hipMemcpyDeviceToHost, stream));
   CK_HIP(hipStreamSynchronize(stream));

@@ -22,6 +22,8 @@ struct Spec {
   float eps = 1e-5f;
   std::vector<int> stem;
   std::vector<std::pair<std::string, int>> outputs;
+  // optional NV12 camera geometry (run_frame_nv12); width 0 = none
+  int cam_w = 0, cam_h = 0, cam_stride = 0, cam_y_height = 0;
   // optional per-plan-entry GEMM configuration {entry: [tile, split]} (A/B probes)
   std::vector<std::pair<std::string, std::pair<int, int>>> gemm_cfg;
 };
@@ -67,6 +69,9 @@ struct ck_engine {
   uint8_t* h_warped = nullptr;   // pinned staging (outlives every async copy)
   float* h_packed = nullptr;
   float* h_out = nullptr;
+  uint8_t* h_nv12 = nullptr;     // pinned staging of the two NV12 frames (camera specs only)
+  float* h_tfm = nullptr;
+  size_t nv12_bytes = 0;         // one NV12 frame
   // derived sizes
   int T = 0, n_spatial = 0, n_head_out = 0, n_out = 0, n_ctx = 0, ld_ctx = 0, packed_len = 0;
   size_t warped_bytes = 0;
@@ -78,6 +83,8 @@ struct ck_engine {
   void* ptr(const std::string& name) { return tensor(name).ptr; }
   void upload(const std::string& name, const void* host, size_t nbytes);
   void run_frame(const uint8_t* warped, const float* packed, float* out);
+  void run_frame_nv12(const uint8_t* frame, const uint8_t* big_frame, const float* tfm, const float* big_tfm,
+                      const float* packed, float* out);
   void frame_launch();
   void capture();
   void drop_graph();

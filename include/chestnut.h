@@ -80,6 +80,15 @@ int ck_decoded_layout(ck_engine* e, int* n, char* buf, size_t len);
  * Replaces: run_frame(warped_np, packed) (run_pinned2.py:1462-1565). */
 int ck_run_frame(ck_engine* e, const uint8_t* warped, const float* packed, float* out);
 
+/* The openpilot flow of one step: two NV12 camera frames (frame_bytes each,
+ * the geometry of the spec's "camera" object) and their f32 [3][3] inverse
+ * transforms are warped on device into `warped` (see ck_warp_nv12), then the
+ * frame runs as in ck_run_frame.  Host pointers.
+ * Replaces: warp(tfm, big_tfm, frame, big_frame) followed by run_policy
+ * (compile_modeld.py:181-221; modeld's per-frame call). */
+int ck_run_frame_nv12(ck_engine* e, const uint8_t* frame, const uint8_t* big_frame, size_t frame_bytes,
+                      const float* tfm, const float* big_tfm, const float* packed, float* out);
+
 /* 1 = replay the plan as one hipGraph launch per frame (default),
  * 0 = launch the plan kernel by kernel.
  * Replaces: REPLAY=1 / REPLAY=0 (run_pinned2.py:1391-1403, 1567-1571). */

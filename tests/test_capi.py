@@ -35,6 +35,14 @@ def test_bad_spec_raises_with_message():
     bad = dict(S.get_spec('tiny'), n_heads=3)
     with pytest.raises(RuntimeError, match='n_heads'):
         _lib.call('ck_create', S.spec_json(bad).encode(), ctypes.byref(ctypes.c_void_p()))
+    odd = dict(S.get_spec('tiny'), camera=dict(S.ROAD_CAMERA, width=1927))
+    with pytest.raises(RuntimeError, match='camera needs an even width'):
+        _lib.call('ck_create', S.spec_json(odd).encode(), ctypes.byref(ctypes.c_void_p()))
+
+
+def test_nv12_bytes():
+    # Y plane 2048 x 1216 plus 604 UV rows of 2048 bytes
+    assert S.nv12_bytes(S.ROAD_CAMERA) == 2048 * 1216 + 604 * 2048
 
 
 def test_kernel_entry_validation_rejects_before_launch():

@@ -221,3 +221,40 @@ def test_1b_frames_vs_oracle(gpu):
                 print(f'[1b] frame {f} {name} rel={e:.2e}', flush=True)
                 assert e <= REL, (f, name, e)
             hs = out[eng.out_slices['hidden_state']]
+
+
+def test_nv12_frames_vs_oracle(gpu):
+    """modeld's flow: NV12 frames + transforms -> device warp -> frame.  The
+    warped input matches the oracle warp bit for bit and the outputs match
+    the oracle model run on the oracle-warped frames."""
+    from oracle import warp as OW
+    cam = dict(width=320, height=200, stride=384, y_height=208)
+    sp = dict(S.get_spec('tiny'), camera=cam)
+    w = S.make_weights(sp)
+    nb = S.nv12_bytes(cam)
+    nv12 = (cam['width'], cam['height'], cam['stride'], cam['y_height'], cam['height'] // 2)
+    rng = np.random.default_rng(21)
+    orc = OM.OracleModel(sp, w)
+    with Engine(sp, weights=w) as eng:
+        eng.reset()
+        pk_dev = None
+        for f, (_, packed) in enumerate(frame_inputs(rng, sp, 3)):
+            frame = rng.integers(0, 256, nb, dtype=np.uint8)
+            big = rng.integers(0, 256, nb, dtype=np.uint8)
+            a = 0.05 * rng.standard_normal()
+            tfm = np.array([[0.6 * np.cos(a), -0.6 * np.sin(a), 8.0], [0.6 * np.sin(a), 0.6 * np.cos(a), 20.0],
+                            [2e-4 * rng.standard_normal(), 2e-4 * rng.standard_normal(), 1.0]], np.float32)
+            big_tfm = np.array([[0.4, 0.02, 60.0], [-0.01, 0.4, 50.0], [0.0, 0.0, 1.0]], np.float32)
+            if pk_dev is not None:
+                packed[12:] = pk_dev
+            print(f'[nv12] frame {f}', flush=True)
+            out = eng.run_frame_nv12(frame, big, tfm, big_tfm, packed)
+            warped = OW.warp(tfm, big_tfm, frame, big, nv12, 2 * sp['img_w'], 2 * sp['img_h'])
+            np.testing.assert_array_equal(eng.read('warped', np.uint8, warped.shape), warped)
+            ref = orc.run_frame(warped, packed)
+            for name, sl in eng.out_slices.items():
+                e = rel_err(out[sl], ref[sl])
+                assert e <= REL, (f, name, e)
+            pk_dev = out[eng.out_slices['hidden_state']]
+        with pytest.raises(ValueError, match='NV12'):
+            eng.run_frame_nv12(frame[:-1], big, tfm, big_tfm, packed)
