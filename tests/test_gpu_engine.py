@@ -258,3 +258,26 @@ def test_nv12_frames_vs_oracle(gpu):
             pk_dev = out[eng.out_slices['hidden_state']]
         with pytest.raises(ValueError, match='NV12'):
             eng.run_frame_nv12(frame[:-1], big, tfm, big_tfm, packed)
+
+
+def test_rows_gate_graph_vs_eager(tiny):
+    """video_check-style rows (video_check.py:47-94): graph replay and plain
+    launches give bit-identical rows over a recurrent clip, and the rows
+    follow the oracle model's outputs."""
+    from chestnut import rows as R
+    sp, w, eng = tiny
+    frames = list(R.synthetic_frames(5, seed=3))
+    eng.reset()
+    a = R.run_rows(eng.run_frame, eng.out_slices, frames)
+    eng.set_graph(False)
+    try:
+        eng.reset()
+        b = R.run_rows(eng.run_frame, eng.out_slices, frames)
+    finally:
+        eng.set_graph(True)
+    ok, first = R.gate(a, b)
+    assert ok, f'first differing row {first}'
+    orc = OM.OracleModel(sp, w)
+    c = R.run_rows(orc.run_frame, eng.out_slices, frames)
+    scale = np.abs(c[:, 1:4]).max()
+    assert np.max(np.abs(a[:, 1:4] - c[:, 1:4])) <= 1e-3 * scale

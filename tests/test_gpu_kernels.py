@@ -193,9 +193,10 @@ def test_gemm_nt_tiles_tails(gpu, tile, M, N, Kd, split):
     _gemm_check(C, A, W, transB=True)
 
 
+@pytest.mark.parametrize('tile', [0, 5, 9])
 @pytest.mark.parametrize('N', [200, 196])
 @pytest.mark.parametrize('epi', [1, 2, 3, 4])
-def test_gemm_epilogues(gpu, epi, N):
+def test_gemm_epilogues(gpu, epi, N, tile):
     from chestnut import kernels as K
     torch = gpu
     rng = np.random.default_rng(epi)
@@ -207,14 +208,14 @@ def test_gemm_epilogues(gpu, epi, N):
     if epi == 4:
         C0 = rng.standard_normal((M, N)).astype(np.float32)
         out = dev(torch, C0.copy())
-        K.gemm_epi(dev(torch, A), dev(torch, W), dev(torch, b), 4, out)
+        K.gemm_epi(dev(torch, A), dev(torch, W), dev(torch, b), 4, out, tile=tile)
         ref = C0 + acc
         got = host(out)
         scale = np.abs(A.astype(np.float64)) @ np.abs(W.astype(np.float64)).T + np.abs(b) + np.abs(C0)
         assert np.all(np.abs(got - ref) <= (Kd // 16 + 40) * U * scale)
         return
     out = torch.empty(M, N, dtype=torch.float16, device='cuda')
-    K.gemm_epi(dev(torch, A), dev(torch, W), dev(torch, b), epi, out)
+    K.gemm_epi(dev(torch, A), dev(torch, W), dev(torch, b), epi, out, tile=tile)
     got = host(out).astype(np.float64)
     if epi == 2:
         acc = np.maximum(acc, 0)
