@@ -120,14 +120,21 @@ def micro(torch):
     wout = torch.empty(2, 6, 128, 256, dtype=torch.uint8, device='cuda')
     geo = dict(cam_w=cam['width'], cam_h=cam['height'], stride=cam['stride'], y_height=cam['y_height'])
     K.warp_nv12(fr[0], fr[1], tfm, tfm, out=wout, **geo)
-    reps = 200
+    # one launch is shorter than a Python call: replay 50 captured launches
     torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(50):
+            K.warp_nv12(fr[0], fr[1], tfm, tfm, out=wout, **geo)
+    g.replay()
+    torch.cuda.synchronize()
+    reps = 10
     e0.record()
     for _ in range(reps):
-        K.warp_nv12(fr[0], fr[1], tfm, tfm, out=wout, **geo)
+        g.replay()
     e1.record()
     torch.cuda.synchronize()
-    us = e0.elapsed_time(e1) * 1e3 / reps
+    us = e0.elapsed_time(e1) * 1e3 / (reps * 50)
     res['warp_nv12'] = {'camera': [cam['width'], cam['height']], 'model': [512, 256], 'us': round(us, 2),
                         'out_bytes': wout.numel()}
     return res
