@@ -480,13 +480,17 @@ void ck_engine::build_plan() {
   // 4. transformer blocks.  The two residual GEMMs (attention output, MLP
   // down) split K and leave f32 partials in the workspace; the LayerNorm that
   // follows each of them adds partials + bias into x before normalising.
-  auto resid_split = [&](int M, int N, int K) {
-    const long tiles = (long)ceil_div(M, 128) * ceil_div(N, 128);
+  // Tiles and splits were chosen on whole frames of the 1B model (a GEMM's
+  // time inside the frame differs from its time in a loop of its own):
+  //   QKV, MLP up: 128x128, one K-group;  O-proj: 128x64 split to fill 256
+  //   workgroups;  MLP down: 128x128, one K-group, split to fill 256.
+  auto resid_split = [&](int M, int N, int K, int bn) {
+    const long tiles = (long)ceil_div(M, 128) * ceil_div(N, bn);
     int s = 1;
     while (tiles * s * 2 <= 256 && K % (128 * s * 2) == 0 && K / (s * 2) >= 512) s *= 2;
     return s;
   };
-  const int s_o = resid_split(T, d, d), s_dn = resid_split(T, d, F);
+  const int s_o = resid_split(T, d, d, 64), s_dn = resid_split(T, d, F, 128);
   ck_engine* self = this;
   const long part_stride = (long)T * d;
   const float* pend_bias = nullptr;   // bias of the GEMM whose partials the next LN must add
@@ -514,7 +518,7 @@ void ck_engine::build_plan() {
     q.A = hb; q.lda = d; q.B = h16(p + "qkv.w"); q.ldb = d; q.C = ptr("qk"); q.ldc = 2 * d;
     q.bias = f32(p + "qkv.b"); q.M = T; q.N = 3 * d; q.K = d; q.epi = EPI_QKV_FRAG;
     q.vt = h16("vt"); q.qk_cols = 2 * d; q.vt_ld = T; q.head_dim = sp.head_dim;
-    q.tile = 1; q.split = 1;   // 128x128 tiles, two K-groups when K allows
+    q.tile = 5; q.split = 1;   // 128x128 tiles, one K-group
     add_gemm(b + "qkv", "gemm_qkv", q);
     const half_t* qk = h16("qk");
     const half_t* vt = h16("vt");
@@ -525,7 +529,7 @@ void ck_engine::build_plan() {
     });
     GemmDesc o;
     o.A = att; o.lda = d; o.B = h16(p + "o.w"); o.ldb = d;
-    o.M = T; o.N = d; o.K = d; o.epi = EPI_PARTIALS; o.tile = 1; o.split = s_o;
+    o.M = T; o.N = d; o.K = d; o.epi = EPI_PARTIALS; o.tile = 2; o.split = s_o;   // 128x64
     pend_split = add_gemm(b + "o", "gemm_partials", o);   // the split actually used (gemm_config may set it)
     pend_bias = f32(p + "o.b");
     add_ln(b + "ln2", f32(p + "ln2.g"), f32(p + "ln2.b"), hb, true);
@@ -536,14 +540,7 @@ void ck_engine::build_plan() {
     add_gemm(b + "up", "gemm_gelu", up);
     GemmDesc dn;
     dn.A = h16("u"); dn.lda = F; dn.B = h16(p + "down.w"); dn.ldb = F;
-    dn.M = T; dn.N = d; dn.K = F; dn.epi = EPI_PARTIALS; dn.tile = 1; dn.split = s_dn;
-    // 256x128 tiles split 8 ways when that still fills 256 workgroups: each
-    // CU loads 3/4 of the bytes a 128x128 split-4 tile needs, for twice the
-    // partials (the LayerNorm after the block adds 8 instead of 4)
-    if (T % 256 == 0 && d % 128 == 0 && (F / 64) % 8 == 0 && F / 8 >= 128 && (T / 256) * (d / 128) * 8 >= 256) {
-      dn.tile = 9;
-      dn.split = 8;
-    }
+    dn.M = T; dn.N = d; dn.K = F; dn.epi = EPI_PARTIALS; dn.tile = 5; dn.split = s_dn;
     pend_split = add_gemm(b + "down", "gemm_partials", dn);
     pend_bias = f32(p + "down.b");
   }
