@@ -1,0 +1,135 @@
+"""Whole-frame tuning of the block GEMMs' tile and split.
+
+A GEMM's time inside the frame differs from its time in a loop of launches
+of its own family (measured on the 1B model: the per-family loop preferred
+two K-groups for QKV and a 256x128 split-8 tile for MLP-down, both of which
+lose on whole frames).  This tool therefore times whole frames: for each
+block GEMM family in turn it builds the engine with every candidate
+(tile, split) applied to all layers through the spec's `gemm_config`, times
+back-to-back graph launches, and keeps the fastest (coordinate descent, the
+families in order).  The result is a `gemm_config` object for the spec.
+
+    python -m chestnut.tune --spec big_driving_1b [--families qkv,o,up,down] [--frames 100] [--out cfg.json]
+
+The reference tunes its kernels with per-kernel variant benches (bench_r62.py,
+bench_alu.py; the `probe` module here mirrors those); this is the frame-level
+step on top of them.
+"""
+import argparse
+import json
+import sys
+import time
+
+import numpy as np
+
+from . import spec as _spec
+
+FAMILIES = ('qkv', 'o', 'up', 'down')
+# tile code -> (rows, columns) of the output tile (the codes of ck_gemm)
+TILES = {1: (128, 128), 2: (128, 64), 3: (64, 128), 4: (64, 64), 5: (128, 128), 6: (128, 64), 7: (64, 128),
+         8: (64, 64), 9: (256, 128)}
+
+
+def shapes(sp):
+    T, d, F = sp['stem'][-1], sp['d_model'], sp['d_ff']
+    return {'qkv': (T, 3 * d, d, 'frag'), 'o': (T, d, d, 'partials'), 'up': (T, F, d, 'f16'),
+            'down': (T, d, F, 'partials')}
+
+
+def candidates(M, N, K, kind, min_wg=64, max_wg=1024):
+    """(tile, split) pairs the engine accepts for this GEMM: K-steps of 64 per
+    split, split only where the epilogue consumes partials (the QKV fragment
+    epilogue needs split 1), the fragment epilogue only on tiles whose N
+    divides, and a grid of min_wg..max_wg workgroups."""
+    out = []
+    for t, (bm, bn) in TILES.items():
+        if kind == 'frag' and (N % bn or M % 32):
+            continue
+        if t == 9 and kind == 'frag':
+            continue
+        for s in (1, 2, 4, 8):
+            if s > 1 and kind != 'partials':
+                continue
+            if K % (64 * s):
+                continue
+            grid = -(-M // bm) * -(-N // bn) * s
+            if min_wg <= grid <= max_wg:
+                out.append((t, s))
+    return out
+
+
+def config_for(sp, choice):
+    cfg = {}
+    for fam, (t, s) in choice.items():
+        for i in range(sp['n_layers']):
+            cfg[f'blk{i}.{fam}'] = [t, s]
+    return cfg
+
+
+def time_frames(sp, weights, frames=100, warmup=10):
+    from .engine import Engine
+    with Engine(sp, weights=weights) as eng:
+        rng = np.random.default_rng(42)
+        w = rng.integers(0, 256, (2, 6, sp['img_h'], sp['img_w']), dtype=np.uint8)
+        p = np.zeros(sp['desire_len'] + 4 + sp['feat_len'], np.float32)
+        p[8:10] = (1.0, 0.0)
+        eng.run_frame(w, p)
+        for _ in range(warmup):
+            eng.frame_launch()
+        eng.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(frames):
+            eng.frame_launch()
+        eng.synchronize()
+        return (time.perf_counter() - t0) * 1e3 / frames
+
+
+def tune(spec='big_driving_1b', families=FAMILIES, frames=100, log=print):
+    """Coordinate descent over the families; returns (gemm_config, best ms, table)."""
+    sp = _spec.get_spec(spec)
+    sp.pop('gemm_config', None)
+    weights = _spec.make_weights(sp)
+    shp = shapes(sp)
+    choice = {}
+    base = time_frames(sp, weights, frames)
+    log(f'[tune] {sp["name"]}: engine defaults {base:.4f} ms/frame')
+    best_ms, table = base, [('defaults', base)]
+    for fam in families:
+        M, N, K, kind = shp[fam]
+        best_c = None
+        for c in candidates(M, N, K, kind):
+            trial = dict(choice, **{fam: c})
+            ms = time_frames(dict(sp, gemm_config=config_for(sp, trial)), weights, frames)
+            table.append((f'{fam}={c[0]},{c[1]} ' + ' '.join(f'{f}={t},{s}' for f, (t, s) in choice.items()), ms))
+            log(f'[tune]   {fam} tile {c[0]} split {c[1]}: {ms:.4f} ms/frame')
+            if ms < best_ms:
+                best_ms, best_c = ms, c
+        if best_c is not None:
+            choice[fam] = best_c
+            log(f'[tune] {fam}: tile {best_c[0]} split {best_c[1]} -> {best_ms:.4f} ms/frame')
+        else:
+            log(f'[tune] {fam}: engine default kept')
+    return config_for(sp, choice), best_ms, table
+
+
+def _main(argv=None):
+    ap = argparse.ArgumentParser(prog='python -m chestnut.tune')
+    ap.add_argument('--spec', default='big_driving_1b')
+    ap.add_argument('--families', default=','.join(FAMILIES))
+    ap.add_argument('--frames', type=int, default=100)
+    ap.add_argument('--out', default=None, help='write the gemm_config object as JSON')
+    a = ap.parse_args(argv)
+    fams = [f for f in a.families.split(',') if f]
+    for f in fams:
+        if f not in FAMILIES:
+            raise SystemExit(f'unknown family {f!r}; choose from {FAMILIES}')
+    cfg, ms, _ = tune(a.spec, fams, a.frames)
+    print(f'[tune] best {ms:.4f} ms/frame ({1e3 / ms:.1f} fps)')
+    if a.out:
+        with open(a.out, 'w') as fh:
+            json.dump(cfg, fh)
+    return 0
+
+
+if __name__ == '__main__':
+    sys.exit(_main())

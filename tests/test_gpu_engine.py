@@ -281,3 +281,16 @@ def test_rows_gate_graph_vs_eager(tiny):
     c = R.run_rows(orc.run_frame, eng.out_slices, frames)
     scale = np.abs(c[:, 1:4]).max()
     assert np.max(np.abs(a[:, 1:4] - c[:, 1:4])) <= 1e-3 * scale
+
+
+def test_frame_tuner_runs(gpu):
+    """chestnut.tune on the 39M model, one family, few frames: every candidate
+    builds and runs, and the returned configuration is one of them."""
+    from chestnut import tune as TU
+    sp = S.get_spec('driving_39m')
+    lines = []
+    cfg, ms, table = TU.tune('driving_39m', ['o'], frames=3, log=lines.append)
+    assert ms > 0 and len(table) >= 2 and lines
+    M, N, K, kind = TU.shapes(sp)['o']
+    cands = TU.candidates(M, N, K, kind)
+    assert all(tuple(v) in cands for v in cfg.values())

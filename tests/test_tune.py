@@ -1,0 +1,27 @@
+"""Candidate generation and config expansion of chestnut.tune (host logic)."""
+from chestnut import spec as S
+from chestnut import tune as TU
+
+
+def test_candidates_respect_epilogue_and_grid():
+    sh = TU.shapes(S.get_spec('big_driving_1b'))
+    M, N, K, kind = sh['qkv']
+    c = TU.candidates(M, N, K, kind)
+    assert (5, 1) in c and (1, 1) in c
+    assert all(s == 1 for _, s in c) and all(t != 9 for t, _ in c)       # fragment epilogue: split 1, no 256-row tile
+    M, N, K, kind = sh['o']
+    c = TU.candidates(M, N, K, kind)
+    assert (2, 2) in c and (1, 4) in c and (4, 1) in c
+    for t, s in c:
+        bm, bn = TU.TILES[t]
+        grid = -(-M // bm) * -(-N // bn) * s
+        assert 64 <= grid <= 1024 and K % (64 * s) == 0
+    M, N, K, kind = sh['up']
+    assert all(s == 1 for _, s in TU.candidates(M, N, K, kind))            # GELU epilogue is not split
+
+
+def test_config_for_every_layer():
+    sp = S.get_spec('driving_39m')
+    cfg = TU.config_for(sp, {'o': (2, 2), 'down': (5, 4)})
+    assert len(cfg) == 2 * sp['n_layers']
+    assert cfg['blk0.o'] == [2, 2] and cfg[f'blk{sp["n_layers"] - 1}.down'] == [5, 4]
