@@ -9,7 +9,8 @@ block GEMM family in turn it builds the engine with every candidate
 back-to-back graph launches, and keeps the fastest (coordinate descent, the
 families in order).  The result is a `gemm_config` object for the spec.
 
-    python -m chestnut.tune --spec big_driving_1b [--families qkv,o,up,down] [--frames 100] [--out cfg.json]
+    python -m chestnut.tune --spec big_driving_1b [--families qkv,o,up,down,stem0,...,embed] [--frames 100]
+                            [--out cfg.json]
 
 The reference tunes its kernels with per-kernel variant benches (bench_r62.py,
 bench_alu.py; the `probe` module here mirrors those); this is the frame-level
@@ -24,36 +25,57 @@ import numpy as np
 
 from . import spec as _spec
 
-FAMILIES = ('qkv', 'o', 'up', 'down')
+FAMILIES = ('qkv', 'o', 'up', 'down')        # per-block GEMMs (every layer gets the choice)
+SINGLE = ('stem0', 'stem1', 'stem2', 'stem3', 'stem4', 'embed')   # once-per-frame GEMMs
 # tile code -> (rows, columns) of the output tile (the codes of ck_gemm)
 TILES = {1: (128, 128), 2: (128, 64), 3: (64, 128), 4: (64, 64), 5: (128, 128), 6: (128, 64), 7: (64, 128),
          8: (64, 64), 9: (256, 128)}
 
 
 def shapes(sp):
+    """family -> (M, N, K, epilogue kind, batch).  Kinds: 'frag' (QKV fragment
+    epilogue, split 1), 'partials' (split-K partials read by the next LN),
+    'f16' (fused activation, split 1), 'reduce' (split allowed, summed by the
+    split-K reduce kernel)."""
     T, d, F = sp['stem'][-1], sp['d_model'], sp['d_ff']
-    return {'qkv': (T, 3 * d, d, 'frag'), 'o': (T, d, d, 'partials'), 'up': (T, F, d, 'f16'),
-            'down': (T, d, F, 'partials')}
+    out = {'qkv': (T, 3 * d, d, 'frag', 1), 'o': (T, d, d, 'partials', 1), 'up': (T, F, d, 'f16', 1),
+           'down': (T, d, F, 'partials', 1)}
+    H, W, C = sp['img_h'], sp['img_w'], 6 * sp['n_frames']
+    for i, co in enumerate(sp['stem']):
+        H, W = (H - 1) // 2 + 1, (W - 1) // 2 + 1
+        out[f'stem{i}'] = (H * W, co, -(-9 * C // 64) * 64, 'reduce', 2)
+        C = co
+    n_spatial = (sp['img_h'] >> len(sp['stem'])) * (sp['img_w'] >> len(sp['stem']))
+    out['embed'] = (T, d, 2 * n_spatial, 'reduce', 1)
+    return out
 
 
-def candidates(M, N, K, kind, min_wg=64, max_wg=1024):
-    """(tile, split) pairs the engine accepts for this GEMM: K-steps of 64 per
-    split, split only where the epilogue consumes partials (the QKV fragment
-    epilogue needs split 1), the fragment epilogue only on tiles whose N
-    divides, and a grid of min_wg..max_wg workgroups."""
+def entry_names(sp, fam):
+    """Plan entries a family's choice applies to."""
+    if fam in FAMILIES:
+        return [f'blk{i}.{fam}' for i in range(sp['n_layers'])]
+    return [f'{fam}.conv'] if fam.startswith('stem') else [fam]
+
+
+def candidates(M, N, K, kind, batch=1, min_wg=64, max_wg=1024):
+    """(tile, split) pairs the engine accepts for this GEMM: splits up to 16
+    that give every split two or more 64-wide K-steps, split only where the
+    epilogue allows it (the QKV fragment and fused-activation epilogues need
+    split 1), the fragment epilogue only on tiles whose N divides, and a grid
+    of min_wg..max_wg workgroups (fewer when the GEMM cannot fill min_wg)."""
     out = []
     for t, (bm, bn) in TILES.items():
         if kind == 'frag' and (N % bn or M % 32):
             continue
         if t == 9 and kind == 'frag':
             continue
-        for s in (1, 2, 4, 8):
-            if s > 1 and kind != 'partials':
+        for s in range(1, 17):
+            if s > 1 and kind not in ('partials', 'reduce'):
                 continue
-            if K % (64 * s):
+            if K % (64 * s) or (s > 1 and K // (64 * s) < 2):
                 continue
-            grid = -(-M // bm) * -(-N // bn) * s
-            if min_wg <= grid <= max_wg:
+            grid = -(-M // bm) * -(-N // bn) * s * batch
+            if min(min_wg, -(-M // 64) * -(-N // 64) * batch) <= grid <= max_wg:
                 out.append((t, s))
     return out
 
@@ -61,8 +83,8 @@ def candidates(M, N, K, kind, min_wg=64, max_wg=1024):
 def config_for(sp, choice):
     cfg = {}
     for fam, (t, s) in choice.items():
-        for i in range(sp['n_layers']):
-            cfg[f'blk{i}.{fam}'] = [t, s]
+        for name in entry_names(sp, fam):
+            cfg[name] = [t, s]
     return cfg
 
 
@@ -95,9 +117,9 @@ def tune(spec='big_driving_1b', families=FAMILIES, frames=100, log=print):
     log(f'[tune] {sp["name"]}: engine defaults {base:.4f} ms/frame')
     best_ms, table = base, [('defaults', base)]
     for fam in families:
-        M, N, K, kind = shp[fam]
+        M, N, K, kind, batch = shp[fam]
         best_c = None
-        for c in candidates(M, N, K, kind):
+        for c in candidates(M, N, K, kind, batch):
             trial = dict(choice, **{fam: c})
             ms = time_frames(dict(sp, gemm_config=config_for(sp, trial)), weights, frames)
             table.append((f'{fam}={c[0]},{c[1]} ' + ' '.join(f'{f}={t},{s}' for f, (t, s) in choice.items()), ms))
@@ -121,8 +143,8 @@ def _main(argv=None):
     a = ap.parse_args(argv)
     fams = [f for f in a.families.split(',') if f]
     for f in fams:
-        if f not in FAMILIES:
-            raise SystemExit(f'unknown family {f!r}; choose from {FAMILIES}')
+        if f not in FAMILIES + SINGLE:
+            raise SystemExit(f'unknown family {f!r}; choose from {FAMILIES + SINGLE}')
     cfg, ms, _ = tune(a.spec, fams, a.frames)
     print(f'[tune] best {ms:.4f} ms/frame ({1e3 / ms:.1f} fps)')
     if a.out:

@@ -291,6 +291,6 @@ def test_frame_tuner_runs(gpu):
     lines = []
     cfg, ms, table = TU.tune('driving_39m', ['o'], frames=3, log=lines.append)
     assert ms > 0 and len(table) >= 2 and lines
-    M, N, K, kind = TU.shapes(sp)['o']
-    cands = TU.candidates(M, N, K, kind)
+    M, N, K, kind, b = TU.shapes(sp)['o']
+    cands = TU.candidates(M, N, K, kind, b)
     assert all(tuple(v) in cands for v in cfg.values())
