@@ -140,6 +140,33 @@ def micro(torch):
     return res
 
 
+def config4_fps(frames=200):
+    """BASELINE config 4 (the 39M analogue, launch-bound): frames/s with the
+    frame replayed as one graph and with plain launches (REPLAY=0), inputs
+    resident, same process."""
+    from chestnut import Engine, spec as S
+    sp = S.get_spec('driving_39m')
+    res = {'workload': 'driving_39m (BASELINE config 4)', 'params': S.param_count(sp)}
+    with Engine(sp) as eng:
+        rng = np.random.default_rng(4)
+        eng.write('warped', rng.integers(0, 256, (2, 6, sp['img_h'], sp['img_w']), dtype=np.uint8))
+        p = np.zeros(sp['desire_len'] + 4 + sp['feat_len'], np.float32)
+        p[8:10] = (1.0, 0.0)
+        eng.write('packed', p)
+        res['launches'] = len(eng.plan())
+        for mode in ('graph', 'eager'):
+            eng.set_graph(mode == 'graph')
+            for _ in range(10):
+                eng.frame_launch()
+            eng.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(frames):
+                eng.frame_launch()
+            eng.synchronize()
+            res[f'{mode}_fps'] = round(frames / (time.perf_counter() - t0), 1)
+    return res
+
+
 def traffic_record(spec_name, fam):
     """HBM bytes per launch of plan family `fam` from the committed PMC
     summary (FETCH_SIZE + WRITE_SIZE passes, copy-calibrated), if one exists
@@ -323,6 +350,9 @@ def main():
         line['micro'] = micro(torch)
         log(f'[bench] micro {line["micro"]}')
     eng.close()
+    if not a.no_micro:
+        line['config4'] = config4_fps()
+        log(f'[bench] config 4 {line["config4"]}')
     if not a.no_cpu:
         line['cpu_baseline'] = cpu_baseline(sp, weights, a.cpu_frames, warped, packed)
         log(f'[bench] cpu baseline {line["cpu_baseline"]}')
