@@ -4,21 +4,22 @@
 //
 // Those kernels are serial K loops whose whole output tile lives in the
 // register file as loop-carried fragments, one block per SM (255 registers).
-// This kernel instead:
-//   * stages A and B tiles (BK = 64) through LDS, double buffered, with
-//     rows padded to 72 halves so the 16-byte MFMA operand reads of 8
-//     consecutive lanes hit distinct banks;
-//   * computes with v_mfma_f32_32x32x16_f16 (wave64; a 2x2 wave grid, each
-//     wave owns a (BM/2)x(BN/2) sub-tile, at most 4 MFMA accumulators of 16
-//     floats);
-//   * splits K over extra workgroups when the output has too few tiles to
-//     fill 256 CUs (the graph-level split-K the reference names as its next
-//     lever, README.md:170-175), writing f32 partials that a second kernel
-//     sums in split order -- deterministic, unlike atomics;
-//   * orders tiles so that consecutive workgroup ids, which the dispatcher
-//     spreads round-robin over the 8 XCDs, are regrouped so each XCD gets a
-//     contiguous run of M-tiles sharing the same B (weight) columns in its L2;
-//   * fuses bias / ReLU / GELU / residual-add / QKV-split epilogues.
+// This file has two kernels instead:
+//   * gemm_dma_kernel (the production path, tile codes 1-9): A and B tiles go
+//     straight from global memory into an S-stage LDS ring with
+//     global_load_lds_dwordx4, XOR-swizzled for conflict-free MFMA operand
+//     reads; v_mfma_f32_32x32x16_f16 on a grid of 64x64 wave tiles; one or two
+//     K-groups; an LDS-staged epilogue (described at the kernel);
+//   * gemm_kernel (tile codes 11-14): register-staged loads with rows padded
+//     to 72 halves, kept for a B operand given as [K][N], which it transposes
+//     in registers.
+// Both split K over extra workgroups when the output has too few tiles to
+// fill 256 CUs (the graph-level split-K the reference names as its next
+// lever, README.md:170-175), writing f32 partials that a reduce kernel -- or
+// the LayerNorm that consumes them -- sums in split order (deterministic,
+// unlike atomics); regroup tiles so each XCD's L2 holds a run of M-tiles
+// sharing the same weight columns; and fuse bias / ReLU / GELU /
+// residual-add / QKV-split epilogues.
 // MFMA 32x32x16 operand layout (lane l of 64): A row l%32, k = 8*(l/32)..+7;
 // B column l%32, same k; D element e of lane l is row 8*(e/4) + 4*(l/32) +
 // e%4, column l%32.  The layout is checked by the MFMA KAT (wmma.hip).
