@@ -344,17 +344,17 @@ __device__ __forceinline__ void dma_issue(const half_t* const* asrc, const half_
 //   V (B operand of P.V: column r = head dim, 8 tokens from 8*g):
 //     vt chunk ((h * hd/16 + j/16) * T/32 + t/32) * 64 + 16*((t%32)/8) + j%16.
 template <int WM, int WN, int FM, int FN, int EPI>
-__device__ __forceinline__ void store_staged(const GemmParams& p, const float16_t (&acc)[FM][FN], char* region,
-                                             int mw, int nw, int sp, int bz, int lane) {
+__device__ __forceinline__ void store_staged(const GemmParams& p, const float16_t (&acc)[FM][FN],
+                                             const float (&bcol)[FN], char* region, int mw, int nw, int sp, int bz,
+                                             int lane) {
   const bool to_ws = p.split > 1 || EPI == EPI_PARTIALS;
-  const float* bias = (!to_ws && p.bias) ? p.bias + bz * p.sBias : nullptr;
   if (to_ws || EPI == EPI_F32 || EPI == EPI_F32_RESID) {
     constexpr int PF = WN + 8;   // floats
     float* st = reinterpret_cast<float*>(region);
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
       const int c = j * 32 + (lane & 31);
-      const float bv = bias && nw + c < p.N ? bias[nw + c] : 0.f;
+      const float bv = bcol[j];
 #pragma unroll
       for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -384,7 +384,7 @@ __device__ __forceinline__ void store_staged(const GemmParams& p, const float16_
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
       const int c = j * 32 + (lane & 31);
-      const float bv = bias && nw + c < p.N ? bias[nw + c] : 0.f;
+      const float bv = bcol[j];
 #pragma unroll
       for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -428,7 +428,7 @@ __device__ __forceinline__ void store_staged(const GemmParams& p, const float16_
 #pragma unroll
   for (int j = 0; j < FN; ++j) {
     const int c = j * 32 + (lane & 31);
-    const float bv = bias && nw + c < p.N ? bias[nw + c] : 0.f;
+    const float bv = bcol[j];
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -544,6 +544,18 @@ __global__ __launch_bounds__(64 * NWG * KG) void gemm_dma_kernel(const GemmParam
   for (int i = 0; i < FM; ++i)
 #pragma unroll
     for (int j = 0; j < FN; ++j) acc[i][j] = float16_t{};
+  // the bias of the lane's epilogue columns, loaded before the K loop so its
+  // latency hides behind the loop (older than every DMA, it has landed by the
+  // first vmcnt wait)
+  float bcol[FN];
+  {
+    const float* bias = (p.split == 1 && EPI != EPI_PARTIALS && p.bias) ? p.bias + bz * p.sBias : nullptr;
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      const int n = n0 + wn * WN + j * 32 + (lane & 31);
+      bcol[j] = (bias && n < p.N) ? bias[n] : 0.f;
+    }
+  }
 
   // group step t is global step KG*t + grp, held in ring stage (KG*t + grp) % S
 #pragma unroll
@@ -639,7 +651,7 @@ __global__ __launch_bounds__(64 * NWG * KG) void gemm_dma_kernel(const GemmParam
   if (p.vec) {
     constexpr int REGION = WM * (WN + 8) * 4;   // bytes per wave; the f32 staging is the largest
     static_assert(NWG * REGION <= S * STAGE * 2, "LDS ring too small for the staged epilogue");
-    store_staged<WM, WN, FM, FN, EPI>(p, acc, reinterpret_cast<char*>(lds) + w4 * REGION, m0 + wm * WM,
+    store_staged<WM, WN, FM, FN, EPI>(p, acc, bcol, reinterpret_cast<char*>(lds) + w4 * REGION, m0 + wm * WM,
                                       n0 + wn * WN, sp, bz, lane);
     return;
   }
