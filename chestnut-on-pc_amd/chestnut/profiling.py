@@ -30,6 +30,8 @@ def _expect(kernel):
     k = kernel.split('+')[0]
     if k.startswith('gemm'):
         return 'gemm'
+    if k.startswith('gemv'):
+        return 'gemv'
     if 'layernorm' in k:
         return 'layernorm'
     return k

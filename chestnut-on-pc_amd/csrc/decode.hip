@@ -27,7 +27,18 @@ __device__ __forceinline__ float safe_exp(float x) { return expf(fminf(x, 11.0f)
 constexpr int MHP_MAX_N = 8;
 
 __global__ __launch_bounds__(256) void decode_kernel(const float* __restrict__ raw, float* __restrict__ dec,
-                                                     const DecodeHead* __restrict__ heads) {
+                                                     const DecodeHead* __restrict__ heads, int n_heads,
+                                                     unsigned* counter, const float* __restrict__ hn,
+                                                     float* __restrict__ feat, int H) {
+  if ((int)blockIdx.x == n_heads) {
+    // end of frame (the last workgroup when a counter is given): advance the
+    // queue frame counter and feed the new hidden state back into the packed
+    // input's prev_feat slot (run_pinned2.py:1580 done on device).  Nothing
+    // else in this launch reads either.
+    if (threadIdx.x == 0) counter[0] = counter[0] + 1u;
+    for (int j = threadIdx.x; j < H; j += 256) feat[j] = hn[j];
+    return;
+  }
   const DecodeHead h = heads[blockIdx.x];
   const float* in = raw + h.in_off;
   float* out = dec + h.out_off;
@@ -126,9 +137,12 @@ __global__ __launch_bounds__(256) void decode_kernel(const float* __restrict__ r
 
 }  // namespace
 
-void launch_decode(const float* raw, float* decoded, const DecodeHead* heads_dev, int n_heads, hipStream_t s) {
+void launch_decode(const float* raw, float* decoded, const DecodeHead* heads_dev, int n_heads, hipStream_t s,
+                   unsigned* counter, const float* h, float* packed_feat, int H) {
   CK_REQUIRE(raw && decoded && heads_dev && n_heads > 0, "decode: bad arguments");
-  hipLaunchKernelGGL(decode_kernel, dim3(n_heads), dim3(256), 0, s, raw, decoded, heads_dev);
+  CK_REQUIRE(!counter || (h && packed_feat && H > 0), "decode: the frame tick needs h, packed_feat and H");
+  hipLaunchKernelGGL(decode_kernel, dim3(n_heads + (counter ? 1 : 0)), dim3(256), 0, s, raw, decoded, heads_dev,
+                     n_heads, counter, h, packed_feat, H);
   CK_LAUNCHED("decode");
 }
 

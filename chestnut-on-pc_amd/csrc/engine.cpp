@@ -466,16 +466,13 @@ void ck_engine::build_plan() {
     const half_t* pos = h16("pos");
     const float* eb = f32("emb.b");
     float* x = f32("x");
-    const int Tt = T;
-    add("embed.init", "embed_init", 0, (double)Tt * d * 6 + d * 8, [=](hipStream_t s) {
-      launch_embed_init(pos, ctx, eb, x, Tt, d, s);
-    });
+    // X0 = F W_emb^T + b + pos + ctx, all in the GEMM's epilogue
     GemmDesc g;
     g.A = tok; g.lda = 2 * ns;
     g.B = h16("emb.w"); g.ldb = 2 * ns;
-    g.C = x; g.ldc = d;
-    g.M = T; g.N = d; g.K = 2 * ns; g.epi = EPI_F32_RESID;
-    add_gemm("embed", "gemm_resid", g);
+    g.C = x; g.ldc = d; g.bias = eb; g.pos = pos; g.ctx = ctx;
+    g.M = T; g.N = d; g.K = 2 * ns; g.epi = EPI_EMBED;
+    add_gemm("embed", "gemm_embed", g);
   }
   // 4. transformer blocks.  The two residual GEMMs (attention output, MLP
   // down) split K and leave f32 partials in the workspace; the LayerNorm that
@@ -559,30 +556,30 @@ void ck_engine::build_plan() {
     const half_t* whh = h16("gru.whh");
     const float* bih = f32("gru.bih");
     const float* bhh = f32("gru.bhh");
-    add("gru.ih", "gemv", 2.0 * 3 * Hh * d, 3.0 * Hh * d * 2, [=](hipStream_t s) {
-      launch_gemv(wih, pooled, bih, gi, 3 * Hh, d, d, GEMV_NONE, 0, s);
+    // gi = W_ih pooled + b_ih and gh = W_hh h_prev + b_hh: one launch
+    add("gru", "gemv2", 2.0 * 3 * Hh * (d + Hh), 3.0 * Hh * (d + Hh) * 2, [=](hipStream_t s) {
+      launch_gemv2(wih, pooled, bih, gi, 3 * Hh, d, whh, hprev, bhh, gh, 3 * Hh, Hh, s);
     });
-    add("gru.hh", "gemv", 2.0 * 3 * Hh * Hh, 3.0 * Hh * Hh * 2, [=](hipStream_t s) {
-      launch_gemv(whh, hprev, bhh, gh, 3 * Hh, Hh, Hh, GEMV_NONE, 0, s);
-    });
+    // heads on the new hidden state; the GRU update is computed inside the
+    // GEMV, which also stores h to h_new and to the output's hidden_state slice
     float* out = f32("out");
     float* hn = f32("h_new");
     const int nho = n_head_out;
-    add("gru.gate", "gru_gate", 0, 8.0 * Hh * 4, [=](hipStream_t s) {
-      launch_gru_gate(gi, gh, hprev, hn, out + nho, Hh, s);
-    });
     const half_t* hw = h16("head.w");
     const float* hbias = f32("head.b");
-    add("heads", "gemv", 2.0 * nho * Hh, (double)nho * Hh * 2, [=](hipStream_t s) {
-      launch_gemv(hw, hn, hbias, out, nho, Hh, Hh, GEMV_NONE, 0, s);
+    add("heads", "gemv_gru", 2.0 * nho * Hh, (double)nho * Hh * 2 + 7.0 * Hh * 4, [=](hipStream_t s) {
+      launch_gemv_gru(hw, hbias, out, nho, gi, gh, hprev, hn, out + nho, Hh, s);
     });
+    // the Parser's decode, and in the same launch the end-of-frame tick:
+    // queue counter + 1, h_new -> packed prev_feat (read by the next frame)
     float* dec = f32("decoded");
     const DecodeHead* dd = dec_dev;
     const int ndh = (int)dec_heads.size();
-    add("decode", "decode", 0, (double)(n_out + n_decoded) * 4, [=](hipStream_t s) { launch_decode(out, dec, dd, ndh, s); });
     unsigned* counter = static_cast<unsigned*>(ptr("counter"));
     float* feat = f32("packed") + dl + 4;
-    add("tick", "frame_tick", 0, 8.0 * Hh, [=](hipStream_t s) { launch_frame_tick(counter, hn, feat, Hh, s); });
+    add("decode", "decode", 0, (double)(n_out + n_decoded) * 4 + 8.0 * Hh, [=](hipStream_t s) {
+      launch_decode(out, dec, dd, ndh, s, counter, hn, feat, Hh);
+    });
   }
   // the split-K workspace is an ordinary activation tensor ("ws"), so state
   // snapshots (probes) see the partials a residual LayerNorm consumes

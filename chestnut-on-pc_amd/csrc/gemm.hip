@@ -46,6 +46,8 @@ struct GemmParams {
   int qk_cols;
   int head_dim;       // EPI_QKV_FRAG
   int vec;            // 1: shapes/alignment allow the LDS-staged 16-byte epilogue
+  const half_t* pos;  // EPI_EMBED
+  const float* ctx;   // EPI_EMBED
 };
 
 template <int EPI>
@@ -53,6 +55,9 @@ __device__ __forceinline__ void epi_store(const GemmParams& p, void* C, const fl
   if (EPI == EPI_F32) {
     if (bias) v += bias[n];
     static_cast<float*>(C)[(long)m * p.ldc + n] = v;
+  } else if (EPI == EPI_EMBED) {
+    if (bias) v += bias[n];
+    static_cast<float*>(C)[(long)m * p.ldc + n] = v + ((float)p.pos[(long)m * p.ldc + n] + p.ctx[n]);
   } else if (EPI == EPI_F32_RESID) {
     if (bias) v += bias[n];
     float* c = static_cast<float*>(C) + (long)m * p.ldc + n;
@@ -217,7 +222,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(const GemmParams p) {
         }
     return;
   }
-  void* C = (EPI == EPI_F32 || EPI == EPI_F32_RESID)
+  void* C = (EPI == EPI_F32 || EPI == EPI_F32_RESID || EPI == EPI_EMBED)
                 ? static_cast<void*>(static_cast<float*>(p.C) + bz * p.sC)
                 : static_cast<void*>(static_cast<half_t*>(p.C) + bz * p.sC);
   const float* bias = p.bias ? p.bias + bz * p.sBias : nullptr;
@@ -262,7 +267,7 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const GemmParams p) 
 #pragma unroll
         for (int e = 0; e < 4; ++e) v[e] += part[i][e];
   }
-  void* C = (EPI == EPI_F32 || EPI == EPI_F32_RESID)
+  void* C = (EPI == EPI_F32 || EPI == EPI_F32_RESID || EPI == EPI_EMBED)
                 ? static_cast<void*>(static_cast<float*>(p.C) + bz * p.sC)
                 : static_cast<void*>(static_cast<half_t*>(p.C) + bz * p.sC);
   const float* bias = p.bias ? p.bias + bz * p.sBias : nullptr;
@@ -348,7 +353,7 @@ __device__ __forceinline__ void store_staged(const GemmParams& p, const float16_
                                              const float (&bcol)[FN], char* region, int mw, int nw, int sp, int bz,
                                              int lane) {
   const bool to_ws = p.split > 1 || EPI == EPI_PARTIALS;
-  if (to_ws || EPI == EPI_F32 || EPI == EPI_F32_RESID) {
+  if (to_ws || EPI == EPI_F32 || EPI == EPI_F32_RESID || EPI == EPI_EMBED) {
     constexpr int PF = WN + 8;   // floats
     float* st = reinterpret_cast<float*>(region);
 #pragma unroll
@@ -374,6 +379,11 @@ __device__ __forceinline__ void store_staged(const GemmParams& p, const float16_
       float4_t v = *reinterpret_cast<const float4_t*>(st + r * PF + c);
       float4_t* g = reinterpret_cast<float4_t*>(dst + (long)m * ld + n);
       if (!to_ws && EPI == EPI_F32_RESID) v += *g;
+      if (!to_ws && EPI == EPI_EMBED) {
+        const half4_t ps = *reinterpret_cast<const half4_t*>(p.pos + (long)m * p.ldc + n);
+        const float4_t cs = *reinterpret_cast<const float4_t*>(p.ctx + n);
+        v += float4_t{(float)ps[0] + cs[0], (float)ps[1] + cs[1], (float)ps[2] + cs[2], (float)ps[3] + cs[3]};
+      }
       __builtin_nontemporal_store(v, g);
     }
     return;
@@ -670,7 +680,7 @@ __global__ __launch_bounds__(64 * NWG * KG) void gemm_dma_kernel(const GemmParam
         }
     return;
   }
-  void* C = (EPI == EPI_F32 || EPI == EPI_F32_RESID)
+  void* C = (EPI == EPI_F32 || EPI == EPI_F32_RESID || EPI == EPI_EMBED)
                 ? static_cast<void*>(static_cast<float*>(p.C) + bz * p.sC)
                 : static_cast<void*>(static_cast<half_t*>(p.C) + bz * p.sC);
   const float* bias = p.bias ? p.bias + bz * p.sBias : nullptr;
@@ -857,6 +867,12 @@ void launch_gemm(GemmDesc d, hipStream_t s) {
   p.Mt = ceil_div(d.M, tile_bm(d.tile)); p.Nt = ceil_div(d.N, tile_bn(d.tile));
   p.qk_cols = d.qk_cols;
   p.head_dim = d.head_dim;
+  p.pos = d.pos;
+  p.ctx = d.ctx;
+  if (d.epi == EPI_EMBED)
+    CK_REQUIRE(d.pos && d.ctx && (reinterpret_cast<uintptr_t>(d.pos) & 7) == 0 &&
+                   (reinterpret_cast<uintptr_t>(d.ctx) & 15) == 0,
+               "gemm: the embedding epilogue needs pos (8-byte aligned) and ctx (16-byte aligned)");
   {
     // the staged epilogue writes 16-byte chunks: 8 halves / 4 floats per chunk
     const auto al16 = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
@@ -864,7 +880,7 @@ void launch_gemm(GemmDesc d, hipStream_t s) {
     if (d.split > 1 || d.epi == EPI_PARTIALS) {
       v = v && al16(d.ws);
     } else {
-      const int el = (d.epi == EPI_F32 || d.epi == EPI_F32_RESID) ? 4 : 8;
+      const int el = (d.epi == EPI_F32 || d.epi == EPI_F32_RESID || d.epi == EPI_EMBED) ? 4 : 8;
       v = v && al16(d.C) && d.ldc % el == 0 && d.sC % el == 0;
       if (d.epi == EPI_QKV || d.epi == EPI_QKV_FRAG)
         v = v && d.qk_cols % tile_bn(d.tile) == 0 && d.M % 8 == 0 && d.vt_ld % 8 == 0 && al16(d.vt);
@@ -904,6 +920,7 @@ void launch_gemm(GemmDesc d, hipStream_t s) {
     case EPI_F16_BIAS_RELU: launch_epi<false, EPI_F16_BIAS_RELU>(d.tile, p, s); if (d.split > 1) launch_reduce<EPI_F16_BIAS_RELU>(p, s); break;
     case EPI_F16_BIAS_GELU: launch_epi<false, EPI_F16_BIAS_GELU>(d.tile, p, s); if (d.split > 1) launch_reduce<EPI_F16_BIAS_GELU>(p, s); break;
     case EPI_F32_RESID: launch_epi<false, EPI_F32_RESID>(d.tile, p, s); if (d.split > 1) launch_reduce<EPI_F32_RESID>(p, s); break;
+    case EPI_EMBED: launch_epi<false, EPI_EMBED>(d.tile, p, s); if (d.split > 1) launch_reduce<EPI_EMBED>(p, s); break;
     case EPI_QKV: launch_epi<false, EPI_QKV>(d.tile, p, s); if (d.split > 1) launch_reduce<EPI_QKV>(p, s); break;
     case EPI_PARTIALS: launch_epi<false, EPI_PARTIALS>(d.tile, p, s); break;
     case EPI_QKV_FRAG: launch_epi<false, EPI_QKV_FRAG>(d.tile, p, s); break;

@@ -20,6 +20,13 @@
 //     wave partials are combined through LDS in wave order.
 // The result is deterministic; relative to the exact sum it carries f32
 // reassociation error only.
+//
+// A launch can carry two independent GEMVs (the GRU's input and hidden
+// products: one launch instead of two), and the input vector can be the GRU
+// update computed on the fly from the gate pre-activations (the heads GEMV
+// after the GRU: the gate kernel is folded into it).
+#include <algorithm>
+
 #include "common.h"
 #include "kernels.h"
 
@@ -30,12 +37,34 @@ constexpr int GEMV_THREADS = 256;
 constexpr int GEMV_STEP_COLS = GEMV_THREADS * 8;   // 2048 columns per step
 constexpr int GEMV_RB = 4;                          // rows per batch
 
-template <int NSTEP>
-__global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(const half_t* __restrict__ W, const float* __restrict__ x,
-                                                            const float* __restrict__ bias, float* __restrict__ y,
-                                                            int rows, int K, int ldw, int rows_per_wg, int act) {
+// One GEMV of a launch.  Workgroups [0, nb0) take the first, the rest the
+// second (when the launch carries two).
+struct GemvArgs {
+  const half_t* W;
+  const float* x;      // input vector (null when GRU-gated)
+  const float* bias;
+  float* y;
+  int rows, K, ldw, rows_per_wg, act;
+  // GRU-gated input (gates r, z, n as rows [0,K), [K,2K), [2K,3K) of gi and
+  // gh, biases included): r = sig(gi_r + gh_r), z = sig(gi_z + gh_z),
+  // n = tanh(gi_n + r * gh_n), x = (1 - z) * n + z * hp.  The first
+  // workgroup also stores x to h1 (and h2 when given).
+  const float* gi;
+  const float* gh;
+  const float* hp;
+  float* h1;
+  float* h2;
+};
+
+template <int NSTEP, bool GATE>
+__global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(const GemvArgs a0, const GemvArgs a1, int nb0) {
   __shared__ float red[2][4][GEMV_RB];
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const bool second = (int)blockIdx.x >= nb0;
+  const GemvArgs& a = second ? a1 : a0;
+  const int blk = second ? (int)blockIdx.x - nb0 : (int)blockIdx.x;
+  const half_t* __restrict__ W = a.W;
+  const int rows = a.rows, K = a.K, ldw = a.ldw;
 
   float xr[NSTEP][8];
   bool cv[NSTEP];
@@ -44,18 +73,36 @@ __global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(const half_t* __rest
     const int c = s * GEMV_STEP_COLS + t * 8;
     cv[s] = c < K;
     if (cv[s]) {
-      float4_t a = *reinterpret_cast<const float4_t*>(x + c);
-      float4_t b = *reinterpret_cast<const float4_t*>(x + c + 4);
-      xr[s][0] = a[0]; xr[s][1] = a[1]; xr[s][2] = a[2]; xr[s][3] = a[3];
-      xr[s][4] = b[0]; xr[s][5] = b[1]; xr[s][6] = b[2]; xr[s][7] = b[3];
+      if (GATE) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const int cj = c + j;
+          const float r = sigmoidf_(a.gi[cj] + a.gh[cj]);
+          const float z = sigmoidf_(a.gi[K + cj] + a.gh[K + cj]);
+          const float n = tanhf(a.gi[2 * K + cj] + r * a.gh[2 * K + cj]);
+          xr[s][j] = (1.0f - z) * n + z * a.hp[cj];
+        }
+        if (blk == 0) {
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            a.h1[c + j] = xr[s][j];
+            if (a.h2) a.h2[c + j] = xr[s][j];
+          }
+        }
+      } else {
+        const float4_t u = *reinterpret_cast<const float4_t*>(a.x + c);
+        const float4_t v = *reinterpret_cast<const float4_t*>(a.x + c + 4);
+        xr[s][0] = u[0]; xr[s][1] = u[1]; xr[s][2] = u[2]; xr[s][3] = u[3];
+        xr[s][4] = v[0]; xr[s][5] = v[1]; xr[s][6] = v[2]; xr[s][7] = v[3];
+      }
     } else {
 #pragma unroll
       for (int j = 0; j < 8; ++j) xr[s][j] = 0.f;
     }
   }
 
-  const int r0 = blockIdx.x * rows_per_wg;
-  const int r1 = min(rows, r0 + rows_per_wg);
+  const int r0 = blk * a.rows_per_wg;
+  const int r1 = min(rows, r0 + a.rows_per_wg);
   int par = 0;
   for (int rb = r0; rb < r1; rb += GEMV_RB, par ^= 1) {
     half8_t w[GEMV_RB][NSTEP];
@@ -72,12 +119,12 @@ __global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(const half_t* __rest
     float acc[GEMV_RB];
 #pragma unroll
     for (int i = 0; i < GEMV_RB; ++i) {
-      float a = 0.f;
+      float v = 0.f;
 #pragma unroll
       for (int s = 0; s < NSTEP; ++s)
 #pragma unroll
-        for (int j = 0; j < 8; ++j) a = fmaf((float)w[i][s][j], xr[s][j], a);
-      acc[i] = wave_sum(a);
+        for (int j = 0; j < 8; ++j) v = fmaf((float)w[i][s][j], xr[s][j], v);
+      acc[i] = wave_sum(v);
     }
     if (lane == 0) {
 #pragma unroll
@@ -86,49 +133,95 @@ __global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(const half_t* __rest
     __syncthreads();
     if (t < GEMV_RB && rb + t < r1) {
       float v = ((red[par][0][t] + red[par][1][t]) + red[par][2][t]) + red[par][3][t];
-      if (bias) v += bias[rb + t];
-      if (act == GEMV_GELU) v = gelu_tanh(v);
-      y[rb + t] = v;
+      if (a.bias) v += a.bias[rb + t];
+      if (a.act == GEMV_GELU) v = gelu_tanh(v);
+      a.y[rb + t] = v;
     }
     // `red` is double-buffered by batch parity: the slot written two batches
     // later is only reused after every thread passed the next barrier.
   }
 }
 
-template <int NSTEP>
-void launch_gemv_n(const half_t* W, const float* x, const float* bias, float* y, int rows, int K, int ldw, int act,
-                   int rpw, hipStream_t s) {
-  const int grid = ceil_div(rows, rpw);
-  hipLaunchKernelGGL(gemv_kernel<NSTEP>, dim3(grid), dim3(GEMV_THREADS), 0, s, W, x, bias, y, rows, K, ldw, rpw, act);
+GemvArgs make_args(const half_t* W, const float* x, const float* bias, float* y, int rows, int K, int ldw, int act,
+                   int rows_per_wg) {
+  GemvArgs a{};
+  a.W = W; a.x = x; a.bias = bias; a.y = y;
+  a.rows = rows; a.K = K; a.ldw = ldw; a.act = act; a.rows_per_wg = rows_per_wg;
+  return a;
+}
+
+void check_args(const GemvArgs& a) {
+  CK_REQUIRE(a.W && a.y && (a.x || a.gi), "gemv: null pointer");
+  CK_REQUIRE(a.rows > 0 && a.K > 0, "gemv: rows and K must be positive");
+  CK_REQUIRE(a.K % 8 == 0, "gemv: K must be a multiple of 8");
+  CK_REQUIRE(a.ldw >= a.K && a.ldw % 8 == 0, "gemv: ldw must be >= K and a multiple of 8");
+  CK_REQUIRE(a.K <= 8 * GEMV_STEP_COLS, "gemv: K above 16384 is not supported");
+  CK_REQUIRE((reinterpret_cast<uintptr_t>(a.W) & 15) == 0 && (reinterpret_cast<uintptr_t>(a.x) & 15) == 0,
+             "gemv: W and x must be 16-byte aligned");
+  CK_REQUIRE(!a.gi || (a.gh && a.hp && a.h1), "gemv: the GRU-gated input needs gi, gh, h_prev and an output for h");
+  CK_REQUIRE(a.act == GEMV_NONE || a.act == GEMV_GELU, "gemv: unknown activation");
+}
+
+int batch_rows(const GemvArgs& a) {
+  int rpw = a.rows_per_wg;
+  if (rpw <= 0) rpw = (a.rows + 1023) / 1024;          // >= 3 workgroups per CU up to 3072 rows
+  return ((rpw + GEMV_RB - 1) / GEMV_RB) * GEMV_RB;    // whole batches
+}
+
+template <int NSTEP, bool GATE>
+void launch_n(GemvArgs a0, GemvArgs a1, bool two, hipStream_t s) {
+  a0.rows_per_wg = batch_rows(a0);
+  const int nb0 = ceil_div(a0.rows, a0.rows_per_wg);
+  int grid = nb0;
+  if (two) {
+    a1.rows_per_wg = batch_rows(a1);
+    grid += ceil_div(a1.rows, a1.rows_per_wg);
+  } else {
+    a1 = a0;
+  }
+  hipLaunchKernelGGL((gemv_kernel<NSTEP, GATE>), dim3(grid), dim3(GEMV_THREADS), 0, s, a0, a1, nb0);
   CK_LAUNCHED("gemv");
+}
+
+template <bool GATE>
+void launch_args(const GemvArgs& a0, const GemvArgs& a1, bool two, hipStream_t s) {
+  const int nstep = ceil_div(two ? std::max(a0.K, a1.K) : a0.K, GEMV_STEP_COLS);
+  switch (nstep) {
+    case 1: launch_n<1, GATE>(a0, a1, two, s); break;
+    case 2: launch_n<2, GATE>(a0, a1, two, s); break;
+    case 3: launch_n<3, GATE>(a0, a1, two, s); break;
+    case 4: launch_n<4, GATE>(a0, a1, two, s); break;
+    case 5: launch_n<5, GATE>(a0, a1, two, s); break;
+    case 6: launch_n<6, GATE>(a0, a1, two, s); break;
+    case 7: launch_n<7, GATE>(a0, a1, two, s); break;
+    default: launch_n<8, GATE>(a0, a1, two, s); break;
+  }
 }
 
 }  // namespace
 
 void launch_gemv(const half_t* W, const float* x, const float* bias, float* y, int rows, int K, int ldw, int act,
                  int rows_per_wg, hipStream_t s) {
-  CK_REQUIRE(W && x && y, "gemv: null pointer");
-  CK_REQUIRE(rows > 0 && K > 0, "gemv: rows and K must be positive");
-  CK_REQUIRE(K % 8 == 0, "gemv: K must be a multiple of 8");
-  CK_REQUIRE(ldw >= K && ldw % 8 == 0, "gemv: ldw must be >= K and a multiple of 8");
-  CK_REQUIRE(K <= 8 * GEMV_STEP_COLS, "gemv: K above 16384 is not supported");
-  CK_REQUIRE((reinterpret_cast<uintptr_t>(W) & 15) == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0,
-             "gemv: W and x must be 16-byte aligned");
-  CK_REQUIRE(act == GEMV_NONE || act == GEMV_GELU, "gemv: unknown activation");
-  int rpw = rows_per_wg;
-  if (rpw <= 0) rpw = (rows + 1023) / 1024;         // >= 3 workgroups per CU up to 3072 rows
-  rpw = ((rpw + GEMV_RB - 1) / GEMV_RB) * GEMV_RB;  // whole batches
-  const int nstep = ceil_div(K, GEMV_STEP_COLS);
-  switch (nstep) {
-    case 1: launch_gemv_n<1>(W, x, bias, y, rows, K, ldw, act, rpw, s); break;
-    case 2: launch_gemv_n<2>(W, x, bias, y, rows, K, ldw, act, rpw, s); break;
-    case 3: launch_gemv_n<3>(W, x, bias, y, rows, K, ldw, act, rpw, s); break;
-    case 4: launch_gemv_n<4>(W, x, bias, y, rows, K, ldw, act, rpw, s); break;
-    case 5: launch_gemv_n<5>(W, x, bias, y, rows, K, ldw, act, rpw, s); break;
-    case 6: launch_gemv_n<6>(W, x, bias, y, rows, K, ldw, act, rpw, s); break;
-    case 7: launch_gemv_n<7>(W, x, bias, y, rows, K, ldw, act, rpw, s); break;
-    default: launch_gemv_n<8>(W, x, bias, y, rows, K, ldw, act, rpw, s); break;
-  }
+  const GemvArgs a = make_args(W, x, bias, y, rows, K, ldw, act, rows_per_wg);
+  check_args(a);
+  launch_args<false>(a, a, false, s);
+}
+
+void launch_gemv2(const half_t* W0, const float* x0, const float* b0, float* y0, int rows0, int K0, const half_t* W1,
+                  const float* x1, const float* b1, float* y1, int rows1, int K1, hipStream_t s) {
+  const GemvArgs a0 = make_args(W0, x0, b0, y0, rows0, K0, K0, GEMV_NONE, 0);
+  const GemvArgs a1 = make_args(W1, x1, b1, y1, rows1, K1, K1, GEMV_NONE, 0);
+  check_args(a0);
+  check_args(a1);
+  launch_args<false>(a0, a1, true, s);
+}
+
+void launch_gemv_gru(const half_t* W, const float* bias, float* y, int rows, const float* gi, const float* gh,
+                     const float* h_prev, float* h_out, float* h_out2, int H, hipStream_t s) {
+  GemvArgs a = make_args(W, nullptr, bias, y, rows, H, H, GEMV_NONE, 0);
+  a.gi = gi; a.gh = gh; a.hp = h_prev; a.h1 = h_out; a.h2 = h_out2;
+  check_args(a);
+  launch_args<true>(a, a, false, s);
 }
 
 }  // namespace ck

@@ -14,6 +14,14 @@ namespace ck {
 enum GemvAct { GEMV_NONE = 0, GEMV_GELU = 1 };
 void launch_gemv(const half_t* W, const float* x, const float* bias, float* y, int rows, int K,
                  int ldw, int act, int rows_per_wg, hipStream_t s);
+// Two independent GEMVs (ldw = K, no activation) in one launch.
+void launch_gemv2(const half_t* W0, const float* x0, const float* b0, float* y0, int rows0, int K0, const half_t* W1,
+                  const float* x1, const float* b1, float* y1, int rows1, int K1, hipStream_t s);
+// y = W . h + bias with h the GRU update of gi, gh (gates r, z, n; biases
+// included) and h_prev, computed inside the GEMV; h is also stored to h_out
+// (and h_out2 when non-null).  W is [rows][H].
+void launch_gemv_gru(const half_t* W, const float* bias, float* y, int rows, const float* gi, const float* gh,
+                     const float* h_prev, float* h_out, float* h_out2, int H, hipStream_t s);
 
 // ---- MFMA GEMM (WMMA attention/projection GEMM analogue) -------------------
 enum Epi {
@@ -25,6 +33,8 @@ enum Epi {
   EPI_QKV = 5,            // f16(acc + bias): n < qk_cols -> C16[m][n], else vt[n-qk_cols][m]
   EPI_PARTIALS = 6,       // raw f32 acc of split s -> ws[s][M][N] (no bias, no reduce); a
                           // consumer (the residual-add LayerNorm) sums the splits
+  EPI_EMBED = 8,          // C32 = acc + bias + pos16[m][n] + ctx[n] (the token embedding:
+                          // position table and the per-frame context vector folded in)
   EPI_QKV_FRAG = 7,       // f16(acc + bias) of a [T][3d] QKV product, written in the MFMA
                           // fragment order the attention kernel loads (see gemm.hip):
                           // Q, K -> C, V -> vt.  Needs head_dim, M % 32 == 0, split 1.
@@ -49,6 +59,8 @@ struct GemmDesc {
   long vt_ld = 0;
   int tile = 0;                // 0 auto; else 1:128x128 2:128x64 3:64x128 4:64x64
   int head_dim = 0;            // EPI_QKV_FRAG only
+  const half_t* pos = nullptr; // EPI_EMBED: f16 [M][N] position table (row stride ldc)
+  const float* ctx = nullptr;  // EPI_EMBED: f32 [N] added to every row
 };
 // Resolves auto tile/split (writes them back) and returns the workspace the
 // launch needs, in floats.
@@ -73,11 +85,6 @@ void launch_add_layernorm(float* x, const float* ws, int nsplit, long split_stri
 // out[n] = mean over rows of x[r][n]; part: colmean_workspace(rows, d) floats.
 size_t colmean_workspace(int rows, int d);
 void launch_colmean(const float* x, float* out, float* part, int rows, int d, hipStream_t s);
-void launch_gru_gate(const float* gi, const float* gh, const float* h_prev, float* h_out, float* h_out2,
-                     int H, hipStream_t s);
-void launch_embed_init(const half_t* pos, const float* ctx, const float* bias, float* X, int T, int d,
-                       hipStream_t s);
-void launch_frame_tick(unsigned* counter, const float* h, float* packed_feat, int H, hipStream_t s);
 void launch_fill_u32(void* p, unsigned v, size_t n_words, hipStream_t s);
 
 // ---- output decode (parse_model_outputs.py Parser on device) -----------------
@@ -90,8 +97,11 @@ struct DecodeHead {
   int width;         // SOFTMAX group width
   int in_N, out_N;   // MHP hypotheses / selections (in_N <= 8, out_N <= 8)
 };
-// One workgroup per head; heads_dev is a device copy of the table.
-void launch_decode(const float* raw, float* decoded, const DecodeHead* heads_dev, int n_heads, hipStream_t s);
+// One workgroup per head; heads_dev is a device copy of the table.  With a
+// counter, one more workgroup does the end-of-frame tick in the same launch:
+// counter + 1 and h -> packed_feat (the prev_feat slot of the next frame).
+void launch_decode(const float* raw, float* decoded, const DecodeHead* heads_dev, int n_heads, hipStream_t s,
+                   unsigned* counter = nullptr, const float* h = nullptr, float* packed_feat = nullptr, int H = 0);
 
 // ---- NV12 perspective warp -> `warped` (compile_modeld.py:53-118, 181-193) ----
 // frame, big_frame: NV12 (Y plane of y_height rows, then the interleaved UV

@@ -212,42 +212,6 @@ __global__ __launch_bounds__(256) void colmean_final_kernel(const float* __restr
   out[c] = s / (float)rows;
 }
 
-// GRU update (gate order r, z, n as rows [0,H), [H,2H), [2H,3H)):
-// r = sig(gi_r + gh_r), z = sig(gi_z + gh_z), n = tanh(gi_n + r * gh_n),
-// h = (1 - z) * n + z * h_prev.  gi, gh already include their biases.
-__global__ __launch_bounds__(256) void gru_gate_kernel(const float* __restrict__ gi, const float* __restrict__ gh,
-                                                       const float* __restrict__ hp, float* __restrict__ h1,
-                                                       float* __restrict__ h2, int H) {
-  const int j = blockIdx.x * 256 + threadIdx.x;
-  if (j >= H) return;
-  const float r = sigmoidf_(gi[j] + gh[j]);
-  const float z = sigmoidf_(gi[H + j] + gh[H + j]);
-  const float n = tanhf(gi[2 * H + j] + r * gh[2 * H + j]);
-  const float h = (1.0f - z) * n + z * hp[j];
-  h1[j] = h;
-  if (h2) h2[j] = h;
-}
-
-// X[t][n] = pos[t][n] + ctx[n] + bias[n] (the embedding GEMM then adds F W^T).
-__global__ __launch_bounds__(256) void embed_init_kernel(const half_t* __restrict__ pos, const float* __restrict__ ctx,
-                                                         const float* __restrict__ bias, float* __restrict__ X, int T,
-                                                         int d) {
-  const long i = (long)blockIdx.x * 256 + threadIdx.x;
-  if (i >= (long)T * d) return;
-  const int n = (int)(i % d);
-  X[i] = ((float)pos[i] + ctx[n]) + bias[n];
-}
-
-// End of frame: advance the queue frame counter and feed the new hidden
-// state back into the packed input's prev_feat slot (the host recurrence of
-// run_pinned2.py:1580, done on device so back-to-back frames need no host).
-__global__ __launch_bounds__(256) void frame_tick_kernel(unsigned* counter, const float* __restrict__ h,
-                                                         float* __restrict__ feat, int H) {
-  const int j = blockIdx.x * 256 + threadIdx.x;
-  if (j == 0) counter[0] = counter[0] + 1u;
-  if (j < H) feat[j] = h[j];
-}
-
 __global__ __launch_bounds__(256) void fill_u32_kernel(unsigned* p, unsigned v, size_t n) {
   const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
   if (i < n) p[i] = v;
@@ -290,25 +254,6 @@ void launch_colmean(const float* x, float* out, float* part, int rows, int d, hi
   CK_LAUNCHED("colmean");
   hipLaunchKernelGGL(colmean_final_kernel, dim3(ceil_div(d, 256)), dim3(256), 0, s, part, out, nparts, rows, d);
   CK_LAUNCHED("colmean");
-}
-
-void launch_gru_gate(const float* gi, const float* gh, const float* h_prev, float* h_out, float* h_out2, int H,
-                     hipStream_t s) {
-  CK_REQUIRE(gi && gh && h_prev && h_out && H > 0, "gru_gate: bad arguments");
-  hipLaunchKernelGGL(gru_gate_kernel, dim3(ceil_div(H, 256)), dim3(256), 0, s, gi, gh, h_prev, h_out, h_out2, H);
-  CK_LAUNCHED("gru_gate");
-}
-
-void launch_embed_init(const half_t* pos, const float* ctx, const float* bias, float* X, int T, int d,
-                       hipStream_t s) {
-  CK_REQUIRE(pos && ctx && bias && X, "embed_init: null pointer");
-  hipLaunchKernelGGL(embed_init_kernel, dim3(ceil_div((long)T * d, 256)), dim3(256), 0, s, pos, ctx, bias, X, T, d);
-  CK_LAUNCHED("embed_init");
-}
-
-void launch_frame_tick(unsigned* counter, const float* h, float* packed_feat, int H, hipStream_t s) {
-  hipLaunchKernelGGL(frame_tick_kernel, dim3(ceil_div(H, 256)), dim3(256), 0, s, counter, h, packed_feat, H);
-  CK_LAUNCHED("frame_tick");
 }
 
 void launch_fill_u32(void* p, unsigned v, size_t n_words, hipStream_t s) {

@@ -159,7 +159,7 @@ def test_kernel_times_cover_plan(tiny):
     assert len(plan) > 20
     assert all(e['ms'] > 0 for e in plan)
     names = [e['name'] for e in plan]
-    assert names[0] == 'inputs' and names[-1] == 'tick' and 'blk0.qkv' in names
+    assert names[0] == 'inputs' and names[-1] == 'decode' and 'blk0.qkv' in names
 
 
 def test_config3_single_block(gpu):
