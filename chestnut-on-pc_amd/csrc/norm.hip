@@ -1,6 +1,6 @@
-// Row LayerNorm, token mean-pool, GRU gate, token-embedding init and the
-// end-of-frame tick.  All HBM-bound elementwise / row kernels; one wave per
-// row where a reduction is needed (DPP wave reductions, no LDS).
+// Row LayerNorm (with the residual update of a split-K GEMM folded in), the
+// token mean-pool and a fill kernel.  HBM-bound row kernels: DPP wave
+// reductions, and for wide rows the four wave sums through LDS.
 #include "common.h"
 #include "kernels.h"
 
