@@ -171,44 +171,56 @@ void gather_launch(const void* img, int A, int B, const int* yx, int n, void* ou
 // ---------------------------------------------------------------------------
 // Layer 1: uint8 planes [batch][C][H][W], each plane an image of A=H rows of
 // B=W one-byte texels; value (u8 - 128) / 128, zero outside the image.
+// Thread per 8 consecutive columns of a patch row: one 16-byte store, and the
+// (tap, channel) pair of each column advanced by increment instead of a
+// division per element (32-bit index math; the host checks the sizes fit).
 __global__ __launch_bounds__(256) void im2col_u8_kernel(const uint8_t* __restrict__ img, int C, int H, int W,
                                                         half_t* __restrict__ patches, int Kp, int Ho, int Wo) {
-  const long i = (long)blockIdx.x * 256 + threadIdx.x;
-  const long per = (long)Ho * Wo * Kp;
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  const int kg = Kp / 8;
+  const int per = Ho * Wo * kg;
   const int b = blockIdx.y;
   if (i >= per) return;
-  const int k = (int)(i % Kp);
-  const long p = i / Kp;
-  half_t v = (half_t)0.f;
-  if (k < 9 * C) {
-    const int tap = k / C, c = k % C;
-    const int ho = (int)(p / Wo), wo = (int)(p % Wo);
-    const int y = 2 * ho - 1 + tap / 3, x = 2 * wo - 1 + tap % 3;
-    const uint8_t* plane = img + ((long)b * C + c) * H * W;
-    const int fl = y * W + x;
-    const int fc = min(max(fl, 0), H * W - 1);
-    const bool valid = (x >= 0) & (x < W) & (y >= 0) & (y < H);
-    const uint8_t u = plane[fc];
-    v = valid ? (half_t)(((float)u - 128.0f) * 0.0078125f) : (half_t)0.f;
+  const int p = i / kg, k0 = (i - p * kg) * 8;
+  const int ho = p / Wo, wo = p - ho * Wo;
+  int tap = k0 / C, c = k0 - tap * C;
+  const uint8_t* base = img + (long)b * C * H * W;
+  half8_t v;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    float f = 0.f;
+    if (tap < 9) {
+      const int y = 2 * ho - 1 + tap / 3, x = 2 * wo - 1 + tap % 3;
+      const int fl = y * W + x;
+      const int fc = min(max(fl, 0), H * W - 1);
+      const bool valid = (x >= 0) & (x < W) & (y >= 0) & (y < H);
+      const uint8_t u = base[(long)c * H * W + fc];
+      f = valid ? ((float)u - 128.0f) * 0.0078125f : 0.f;
+    }
+    v[e] = (half_t)f;
+    if (++c == C) {
+      c = 0;
+      ++tap;
+    }
   }
-  patches[(long)b * per + i] = v;
+  *reinterpret_cast<half8_t*>(patches + ((long)b * Ho * Wo + p) * Kp + k0) = v;
 }
 
 // Later layers: f16 activations [batch][H][W][C] = an image of A=H rows of
 // B=W*C/4 texels of 4 halves.  Thread per 4-column texel of the patch row.
 __global__ __launch_bounds__(256) void im2col_f16_kernel(const half_t* __restrict__ act, int C, int H, int W,
                                                          half_t* __restrict__ patches, int Kp, int Ho, int Wo) {
-  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  const int i = blockIdx.x * 256 + threadIdx.x;
   const int kq = Kp / 4;
-  const long per = (long)Ho * Wo * kq;
+  const int per = Ho * Wo * kq;
   const int b = blockIdx.y;
   if (i >= per) return;
-  const int k = (int)(i % kq) * 4;
-  const long p = i / kq;
+  const int p = i / kq;
+  const int k = (i - p * kq) * 4;
   u32x2_t v = {0u, 0u};
   if (k < 9 * C) {
-    const int tap = k / C, c = k % C;
-    const int ho = (int)(p / Wo), wo = (int)(p % Wo);
+    const int tap = k / C, c = k - tap * C;
+    const int ho = p / Wo, wo = p - ho * Wo;
     const int y = 2 * ho - 1 + tap / 3, xs = 2 * wo - 1 + tap % 3;
     const int B = W * (C / 4);
     // texel column: xs = -1 gives x in [-C/4, 0), xs = W gives x >= B, so the
@@ -292,9 +304,11 @@ void launch_img_gather(const void* img, int A, int B, int lanes, int elem_bytes,
 
 void launch_im2col_u8(const uint8_t* img, int batch, int C, int H, int W, half_t* patches, int Kp, hipStream_t s) {
   CK_REQUIRE(img && patches && batch > 0, "im2col_u8: bad arguments");
-  CK_REQUIRE(Kp >= 9 * C, "im2col_u8: Kp too small");
+  CK_REQUIRE(Kp >= 9 * C && Kp % 8 == 0, "im2col_u8: Kp must be >= 9C and a multiple of 8");
+  CK_REQUIRE((reinterpret_cast<uintptr_t>(patches) & 15) == 0, "im2col_u8: patches must be 16-byte aligned");
   const int Ho = (H - 1) / 2 + 1, Wo = (W - 1) / 2 + 1;
-  const long per = (long)Ho * Wo * Kp;
+  const long per = (long)Ho * Wo * (Kp / 8);
+  CK_REQUIRE(per < (1L << 31) && (long)H * W < (1L << 31), "im2col_u8: image too large");
   hipLaunchKernelGGL(im2col_u8_kernel, dim3(ceil_div(per, 256), batch), dim3(256), 0, s, img, C, H, W, patches, Kp,
                      Ho, Wo);
   CK_LAUNCHED("im2col_u8");
@@ -305,6 +319,7 @@ void launch_im2col_f16(const half_t* act, int batch, int C, int H, int W, half_t
   CK_REQUIRE(C % 4 == 0 && Kp % 4 == 0 && Kp >= 9 * C, "im2col_f16: C and Kp must be multiples of 4, Kp >= 9C");
   const int Ho = (H - 1) / 2 + 1, Wo = (W - 1) / 2 + 1;
   const long per = (long)Ho * Wo * (Kp / 4);
+  CK_REQUIRE(per < (1L << 31), "im2col_f16: image too large");
   hipLaunchKernelGGL(im2col_f16_kernel, dim3(ceil_div(per, 256), batch), dim3(256), 0, s, act, C, H, W, patches, Kp,
                      Ho, Wo);
   CK_LAUNCHED("im2col_f16");
