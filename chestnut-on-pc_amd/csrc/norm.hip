@@ -1,6 +1,8 @@
 // Row LayerNorm (with the residual update of a split-K GEMM folded in), the
 // token mean-pool and a fill kernel.  HBM-bound row kernels: DPP wave
 // reductions, and for wide rows the four wave sums through LDS.
+#include <type_traits>
+
 #include "common.h"
 #include "kernels.h"
 
@@ -64,7 +66,9 @@ __global__ __launch_bounds__(256) void layernorm_kernel(float* __restrict__ x, c
 // order.  Row sums: DPP wave sums, then the 4 wave sums through LDS in order.
 constexpr int LN_MAXS = 8;
 
-template <int EPT, bool OUT_F16, bool ADD>
+// NS: 0 no residual update; > 0 exactly NS partials (loads unconditional);
+// -1 up to LN_MAXS partials, count at run time.
+template <int EPT, bool OUT_F16, int NS>
 __global__ __launch_bounds__(256) void layernorm_row_kernel(float* __restrict__ x, const float* __restrict__ ws,
                                                             int nsplit, long split_stride,
                                                             const float* __restrict__ rbias,
@@ -86,14 +90,16 @@ __global__ __launch_bounds__(256) void layernorm_row_kernel(float* __restrict__ 
     gv[j] = *reinterpret_cast<const vec_t*>(g + c);
     bv[j] = *reinterpret_cast<const vec_t*>(b + c);
   }
-  if (ADD) {
-    vec_t p[LN_MAXS][NV], rb[NV];
+  if (NS != 0) {
+    constexpr int KN = NS > 0 ? NS : LN_MAXS;
+    vec_t p[KN][NV], rb[NV];
     const float* w = ws + (long)row * D;
 #pragma unroll
-    for (int k = 0; k < LN_MAXS; ++k)
+    for (int k = 0; k < KN; ++k)
 #pragma unroll
       for (int j = 0; j < NV; ++j)
-        p[k][j] = k < nsplit ? *reinterpret_cast<const vec_t*>(w + k * split_stride + (j * 256 + tid) * VW) : vec_t{};
+        p[k][j] = (NS > 0 || k < nsplit) ? *reinterpret_cast<const vec_t*>(w + k * split_stride + (j * 256 + tid) * VW)
+                                         : vec_t{};
 #pragma unroll
     for (int j = 0; j < NV; ++j)
       rb[j] = rbias ? *reinterpret_cast<const vec_t*>(rbias + (j * 256 + tid) * VW) : vec_t{};
@@ -101,8 +107,8 @@ __global__ __launch_bounds__(256) void layernorm_row_kernel(float* __restrict__ 
     for (int j = 0; j < NV; ++j) {
       vec_t a = p[0][j];
 #pragma unroll
-      for (int k = 1; k < LN_MAXS; ++k)
-        if (k < nsplit) a += p[k][j];
+      for (int k = 1; k < KN; ++k)
+        if (NS > 0 || k < nsplit) a += p[k][j];
       if (rbias) a += rb[j];
       v[j] = v[j] + a;
       *reinterpret_cast<vec_t*>(xr + (j * 256 + tid) * VW) = v[j];
@@ -151,13 +157,16 @@ template <int EPT>
 void ln_row_launch(float* x, const float* ws, int nsplit, long sstride, const float* rbias, const float* g,
                    const float* b, void* out, bool f16, int rows, float eps, hipStream_t s) {
   dim3 grid(rows);
-  if (ws) {
-    if (f16) hipLaunchKernelGGL((layernorm_row_kernel<EPT, true, true>), grid, dim3(256), 0, s, x, ws, nsplit, sstride, rbias, g, b, out, eps);
-    else hipLaunchKernelGGL((layernorm_row_kernel<EPT, false, true>), grid, dim3(256), 0, s, x, ws, nsplit, sstride, rbias, g, b, out, eps);
-  } else {
-    if (f16) hipLaunchKernelGGL((layernorm_row_kernel<EPT, true, false>), grid, dim3(256), 0, s, x, ws, nsplit, sstride, rbias, g, b, out, eps);
-    else hipLaunchKernelGGL((layernorm_row_kernel<EPT, false, false>), grid, dim3(256), 0, s, x, ws, nsplit, sstride, rbias, g, b, out, eps);
-  }
+  auto go = [&](auto ns) {
+    constexpr int NS = decltype(ns)::value;
+    if (f16) hipLaunchKernelGGL((layernorm_row_kernel<EPT, true, NS>), grid, dim3(256), 0, s, x, ws, nsplit, sstride, rbias, g, b, out, eps);
+    else hipLaunchKernelGGL((layernorm_row_kernel<EPT, false, NS>), grid, dim3(256), 0, s, x, ws, nsplit, sstride, rbias, g, b, out, eps);
+  };
+  if (!ws) go(std::integral_constant<int, 0>{});
+  else if (nsplit == 1) go(std::integral_constant<int, 1>{});
+  else if (nsplit == 2) go(std::integral_constant<int, 2>{});
+  else if (nsplit == 4) go(std::integral_constant<int, 4>{});
+  else go(std::integral_constant<int, -1>{});
   CK_LAUNCHED("layernorm_row");
 }
 
