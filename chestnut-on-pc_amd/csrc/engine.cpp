@@ -472,6 +472,7 @@ void ck_engine::build_plan() {
     g.B = h16("emb.w"); g.ldb = 2 * ns;
     g.C = x; g.ldc = d; g.bias = eb; g.pos = pos; g.ctx = ctx;
     g.M = T; g.N = d; g.K = 2 * ns; g.epi = EPI_EMBED;
+    g.tile = 4;   // 64x64: a one- or two-step GEMM whose time is its epilogue, spread over 4x the workgroups
     add_gemm("embed", "gemm_embed", g);
   }
   // 4. transformer blocks.  The two residual GEMMs (attention output, MLP
