@@ -111,15 +111,18 @@ __device__ __forceinline__ float gelu_tanh(float x) {
   return 0.5f * x * (1.0f + tanhf(c * (x + 0.044715f * x * x * x)));
 }
 
-// Same tanh-form GELU with tanh(u) = 1 - 2 / (1 + e^{2u}) on the hardware
-// exponential and reciprocal (v_exp_f32, v_rcp_f32): a few instructions
-// instead of the libm tanh and an IEEE division.  The absolute error of the
-// tanh term is ~1e-7, far below the f16 rounding of the GEMM epilogue that
-// consumes it.
+// Same tanh-form GELU in its sigmoid form, 0.5 x (1 + tanh(u)) = x / (1 + e^{-2u}),
+// with e^{-2u} = 2^(x (c0 + c1 x^2)), c0 = -2 sqrt(2/pi) log2(e), c1 = 0.044715 c0,
+// on the hardware exp2 and reciprocal (v_exp_f32, v_rcp_f32): four VALU
+// operations and two transcendentals per element (the GEMM epilogue runs it
+// on every output, so the count sets the epilogue's time).  Large |x| saturate
+// to x and -0 through inf/0 of the exp2.  The relative error is ~1e-7, far
+// below the f16 rounding of the GEMM epilogue that consumes it.
 __device__ __forceinline__ float gelu_fast(float x) {
-  const float c2 = 2.0f * 0.7978845608028654f;
-  const float t = 1.0f - 2.0f * __builtin_amdgcn_rcpf(1.0f + __expf(c2 * (x + 0.044715f * x * x * x)));
-  return 0.5f * x * (1.0f + t);
+  constexpr float c0 = -2.0f * 0.7978845608028654f * 1.4426950408889634f;
+  constexpr float c1 = 0.044715f * c0;
+  const float z = x * __builtin_fmaf(c1, x * x, c0);
+  return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(z));
 }
 
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); }
