@@ -410,15 +410,19 @@ __device__ __forceinline__ void store_staged(const GemmParams& p, const float16_
     if (EPI == EPI_QKV_FRAG) {
       // V fragment blocks: 16 features x 32 tokens = 64 lanes x 8 tokens, one
       // contiguous KB per block (see the layout note at the epilogue modes)
-      const int r = lane & 15, g = lane >> 4, HDh = p.head_dim;
+      // The wave's WN columns lie in one head (head_dim is a power of two >= WN,
+      // checked on the host), so the head and the first 16-feature block are
+      // wave-uniform and the chunk index is shifts and adds.
+      const int r = lane & 15, g = lane >> 4, hs = __builtin_ctz(p.head_dim);
+      const int f0 = nw - p.qk_cols, h = f0 >> hs, c0 = f0 & (p.head_dim - 1);
+      const long cbase = (long)(h << (hs - 4)) + (c0 >> 4);   // 16-feature block of the wave's first column
+      const int tpb = p.M >> 5;                                 // 32-token blocks
 #pragma unroll
       for (int blk = 0; blk < (WN / 16) * (WM / 32); ++blk) {
         const int cb = blk % (WN / 16), tb = blk / (WN / 16);
         if (mw + tb * 32 >= p.M) continue;
         const int nl = cb * 16 + r, ml = tb * 32 + g * 8;
-        const int f = nw + nl - p.qk_cols, m = mw + ml;
-        const int h = f / HDh, c = f % HDh;
-        const long chunk = ((long)(h * (HDh / 16) + c / 16) * (p.M / 32) + m / 32) * 64 + g * 16 + r;
+        const long chunk = ((cbase + cb) * tpb + (mw >> 5) + tb) * 64 + g * 16 + r;
         *reinterpret_cast<half8_t*>(p.vt + chunk * 8) = *reinterpret_cast<const half8_t*>(st + nl * PT + ml);
       }
       return;
@@ -453,15 +457,18 @@ __device__ __forceinline__ void store_staged(const GemmParams& p, const float16_
   asm volatile("" ::: "memory");
   if (EPI == EPI_QKV_FRAG) {
     // Q / K fragment blocks: 16 tokens x 32 features = 64 lanes x 8 features
-    const int r = lane & 15, g = lane >> 4, HDh = p.head_dim, dh = p.qk_cols / 2, H = dh / HDh;
+    // Q or K, the head and the first 32-feature block are wave-uniform (the
+    // wave's WN columns lie in one head, as for V above).
+    const int r = lane & 15, g = lane >> 4, hs = __builtin_ctz(p.head_dim), dh = p.qk_cols >> 1;
+    const int which = nw >= dh, f0 = nw - which * dh, h = f0 >> hs, c0 = f0 & (p.head_dim - 1);
+    const long hbase = (long)(which * (dh >> hs) + h) * (p.M >> 4);   // 16-token blocks before this head
+    const int kpb = p.head_dim >> 5;                                  // 32-feature blocks per head
 #pragma unroll
     for (int blk = 0; blk < (WM / 16) * (WN / 32); ++blk) {
       const int tb = blk % (WM / 16), kb = blk / (WM / 16);
       if (mw + tb * 16 >= p.M) continue;
       const int ml = tb * 16 + r, nl = kb * 32 + g * 8;
-      const int m = mw + ml, n = nw + nl;
-      const int which = n / dh, f = n % dh, h = f / HDh, c = f % HDh;
-      const long chunk = (((long)(which * H + h) * (p.M / 16) + m / 16) * (HDh / 32) + c / 32) * 64 + g * 16 + r;
+      const long chunk = ((hbase + (mw >> 4) + tb) * kpb + (c0 >> 5) + kb) * 64 + g * 16 + r;
       *reinterpret_cast<half8_t*>(static_cast<half_t*>(p.C) + chunk * 8) =
           *reinterpret_cast<const half8_t*>(st + ml * PH + nl);
     }
@@ -889,9 +896,11 @@ void launch_gemm(GemmDesc d, hipStream_t s) {
   }
   if (d.epi == EPI_QKV_FRAG) {
     const int dh = d.qk_cols / 2;
-    CK_REQUIRE(d.head_dim > 0 && d.head_dim % 32 == 0 && d.qk_cols % 2 == 0 && dh % d.head_dim == 0 &&
-                   d.N == 3 * dh && d.M % 32 == 0 && d.N % tile_bn(d.tile) == 0,
-               "gemm: QKV fragment epilogue needs N = 3d, d % head_dim == 0, head_dim % 32 == 0, M % 32 == 0");
+    const int wn = tile_bn(d.tile) / 2;   // columns per wave
+    CK_REQUIRE(d.head_dim >= wn && (d.head_dim & (d.head_dim - 1)) == 0 && d.qk_cols % 2 == 0 &&
+                   dh % d.head_dim == 0 && d.N == 3 * dh && d.M % 32 == 0 && d.N % tile_bn(d.tile) == 0,
+               "gemm: QKV fragment epilogue needs N = 3d, d % head_dim == 0, head_dim a power of two no smaller "
+               "than a wave's columns, M % 32 == 0");
     CK_REQUIRE(d.split == 1 && d.batch == 1 && tile_dma(d.tile) && p.vec,
                "gemm: QKV fragment epilogue needs split 1, batch 1, an LDS-DMA tile and aligned outputs");
   }
