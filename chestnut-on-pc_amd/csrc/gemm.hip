@@ -346,8 +346,10 @@ __device__ __forceinline__ void dma_issue(const half_t* const* asrc, const half_
 //   Q, K (16x16x32 A/B operand: row r = token, 8 head dims from 8*g):
 //     C chunk (((w*H + h) * T/16 + t/16) * hd/32 + j/32) * 64 + 16*((j%32)/8) + t%16
 //     for token t, head dim j of head h; w = 0 for Q, 1 for K.
-//   V (B operand of P.V: column r = head dim, 8 tokens from 8*g):
-//     vt chunk ((h * hd/16 + j/16) * T/32 + t/32) * 64 + 16*((t%32)/8) + j%16.
+//   V (B operand of P.V: column r = head dim, tokens 4g..4g+3 and
+//   16+4g..16+4g+3 of a 32-token block, the attention kernel's key order):
+//     vt chunk ((h * hd/16 + j/16) * T/32 + t/32) * 64 + 16*((t%16)/4) + j%16,
+//     element (t/16)*4 + t%4 of the chunk.
 template <int WM, int WN, int FM, int FN, int EPI>
 __device__ __forceinline__ void store_staged(const GemmParams& p, const float16_t (&acc)[FM][FN],
                                              const float (&bcol)[FN], char* region, int mw, int nw, int sp, int bz,
@@ -421,9 +423,13 @@ __device__ __forceinline__ void store_staged(const GemmParams& p, const float16_
       for (int blk = 0; blk < (WN / 16) * (WM / 32); ++blk) {
         const int cb = blk % (WN / 16), tb = blk / (WN / 16);
         if (mw + tb * 32 >= p.M) continue;
-        const int nl = cb * 16 + r, ml = tb * 32 + g * 8;
+        // tokens 4g..4g+3 and 16+4g..16+4g+3 of the 32-token block: the key
+        // order in which the attention kernel's P.V A operand leaves its softmax
+        const int nl = cb * 16 + r, ml = tb * 32 + g * 4;
         const long chunk = ((cbase + cb) * tpb + (mw >> 5) + tb) * 64 + g * 16 + r;
-        *reinterpret_cast<half8_t*>(p.vt + chunk * 8) = *reinterpret_cast<const half8_t*>(st + nl * PT + ml);
+        const half4_t lo = *reinterpret_cast<const half4_t*>(st + nl * PT + ml);
+        const half4_t hi = *reinterpret_cast<const half4_t*>(st + nl * PT + ml + 16);
+        *reinterpret_cast<half8_t*>(p.vt + chunk * 8) = half8_t{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
       }
       return;
     }
