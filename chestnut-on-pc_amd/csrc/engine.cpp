@@ -346,7 +346,6 @@ void ck_engine::build_activations() {
   add_tensor("u", (long)T * sp.d_ff * 2, DT_F16, false);
   add_tensor("xf", (long)T * d * 4, DT_F32, false);
   add_tensor("pooled", (long)d * 4, DT_F32, false);
-  add_tensor("pool_part", colmean_workspace(T, d) * 4, DT_F32, false);
   add_tensor("gi", 3L * sp.hidden * 4, DT_F32, false);
   add_tensor("gh", 3L * sp.hidden * 4, DT_F32, false);
   add_tensor("h_new", (long)sp.hidden * 4, DT_F32, false);
@@ -546,10 +545,9 @@ void ck_engine::build_plan() {
   {
     float* xf = f32("xf");
     float* pooled = f32("pooled");
-    float* pp = f32("pool_part");
     const int Tt = T;
     add_ln("final.ln", f32("lnf.g"), f32("lnf.b"), xf, false);
-    add("final.pool", "colmean", 0, (double)Tt * d * 4, [=](hipStream_t s) { launch_colmean(xf, pooled, pp, Tt, d, s); });
+    add("final.pool", "colmean", 0, (double)Tt * d * 4, [=](hipStream_t s) { launch_colmean(xf, pooled, Tt, d, s); });
     const float* hprev = f32("packed") + dl + 4;
     float* gi = f32("gi");
     float* gh = f32("gh");

@@ -82,9 +82,8 @@ void launch_layernorm(const float* x, const float* g, const float* b, void* out,
 // the GEMM that produced x's update; ws[k] at ws + k*split_stride), then LN.
 void launch_add_layernorm(float* x, const float* ws, int nsplit, long split_stride, const float* rbias, const float* g,
                           const float* b, void* out, bool out_f16, int rows, int d, float eps, hipStream_t s);
-// out[n] = mean over rows of x[r][n]; part: colmean_workspace(rows, d) floats.
-size_t colmean_workspace(int rows, int d);
-void launch_colmean(const float* x, float* out, float* part, int rows, int d, hipStream_t s);
+// out[n] = mean over rows of x[r][n] (d % 32 == 0), deterministic.
+void launch_colmean(const float* x, float* out, int rows, int d, hipStream_t s);
 void launch_fill_u32(void* p, unsigned v, size_t n_words, hipStream_t s);
 
 // ---- output decode (parse_model_outputs.py Parser on device) -----------------

@@ -184,41 +184,40 @@ void ln_launch(float* x, const float* ws, int nsplit, long sstride, const float*
   CK_LAUNCHED("layernorm");
 }
 
-// Column mean (mean-pool over tokens) in two deterministic passes.  Pass 1:
-// one wave per block of 256 columns x 16 rows, float4 per lane, sums its 16
-// rows in row order into part[row block][column].  Pass 2 adds the row-block
-// partials of each column in block order and divides by the row count.  (A
-// single pass with a few long column walks leaves most CUs idle and each
-// lane waiting on one load after another.)
-constexpr int COLMEAN_ROWS = 16;
+// Column mean (mean-pool over tokens) in one deterministic pass.  A block of
+// 256 threads owns 32 columns: thread t sums rows t/8, t/8 + 32, ... of the
+// 4 columns 4*(t%8) .. +3 (all of its float4 loads issued before the adds,
+// 16 in flight at 512 rows), then the 32 row-slice sums of each column are
+// added through LDS in slice order and divided by the row count.  d = 2048
+// gives 64 blocks.
+constexpr int COLMEAN_COLS = 32;
+constexpr int COLMEAN_BATCH = 16;   // loads in flight per thread
 
-__global__ __launch_bounds__(64) void colmean_part_kernel(const float* __restrict__ x, float* __restrict__ part,
-                                                         int rows, int d) {
-  const int c = blockIdx.x * 256 + threadIdx.x * 4;
-  const int r0 = blockIdx.y * COLMEAN_ROWS;
-  if (c >= d) return;
+__global__ __launch_bounds__(256) void colmean_kernel(const float* __restrict__ x, float* __restrict__ out, int rows,
+                                                      int d) {
+  __shared__ float red[32][COLMEAN_COLS + 1];
+  const int t = threadIdx.x, cg = t & 7, rs = t >> 3;
+  const int c = blockIdx.x * COLMEAN_COLS + cg * 4;
   float4_t s = {0.f, 0.f, 0.f, 0.f};
+  for (int r0 = rs; r0 < rows; r0 += 32 * COLMEAN_BATCH) {
+    float4_t v[COLMEAN_BATCH];
 #pragma unroll
-  for (int i = 0; i < COLMEAN_ROWS; ++i)
-    if (r0 + i < rows) s += *reinterpret_cast<const float4_t*>(x + (long)(r0 + i) * d + c);
-  *reinterpret_cast<float4_t*>(part + (long)blockIdx.y * d + c) = s;
-}
-
-__global__ __launch_bounds__(256) void colmean_final_kernel(const float* __restrict__ part, float* __restrict__ out,
-                                                           int nparts, int rows, int d) {
-  const int c = blockIdx.x * 256 + threadIdx.x;
-  if (c >= d) return;
-  // the partials are loaded in batches of 32 before they are added (in
-  // block order): one load latency per batch instead of one per partial
-  float s = 0.f;
-  for (int p0 = 0; p0 < nparts; p0 += 32) {
-    float v[32];
+    for (int k = 0; k < COLMEAN_BATCH; ++k) {
+      const int r = r0 + 32 * k;
+      v[k] = r < rows ? *reinterpret_cast<const float4_t*>(x + (long)r * d + c) : float4_t{0.f, 0.f, 0.f, 0.f};
+    }
 #pragma unroll
-    for (int i = 0; i < 32; ++i) v[i] = p0 + i < nparts ? part[(long)(p0 + i) * d + c] : 0.f;
-#pragma unroll
-    for (int i = 0; i < 32; ++i) s += v[i];
+    for (int k = 0; k < COLMEAN_BATCH; ++k) s += v[k];
   }
-  out[c] = s / (float)rows;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) red[rs][cg * 4 + e] = s[e];
+  __syncthreads();
+  if (t < COLMEAN_COLS) {
+    float a = 0.f;
+#pragma unroll 8
+    for (int i = 0; i < 32; ++i) a += red[i][t];
+    out[blockIdx.x * COLMEAN_COLS + t] = a / (float)rows;
+  }
 }
 
 __global__ __launch_bounds__(256) void fill_u32_kernel(unsigned* p, unsigned v, size_t n) {
@@ -252,16 +251,11 @@ void launch_add_layernorm(float* x, const float* ws, int nsplit, long split_stri
   }
 }
 
-size_t colmean_workspace(int rows, int d) { return (size_t)ceil_div(rows, COLMEAN_ROWS) * d; }
-
-void launch_colmean(const float* x, float* out, float* part, int rows, int d, hipStream_t s) {
-  CK_REQUIRE(x && out && part && rows > 0 && d > 0, "colmean: bad arguments");
-  CK_REQUIRE(d % 4 == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0 && (reinterpret_cast<uintptr_t>(part) & 15) == 0,
-             "colmean: d must be a multiple of 4, x and the workspace 16-byte aligned");
-  const int nparts = ceil_div(rows, COLMEAN_ROWS);
-  hipLaunchKernelGGL(colmean_part_kernel, dim3(ceil_div(d, 256), nparts), dim3(64), 0, s, x, part, rows, d);
-  CK_LAUNCHED("colmean");
-  hipLaunchKernelGGL(colmean_final_kernel, dim3(ceil_div(d, 256)), dim3(256), 0, s, part, out, nparts, rows, d);
+void launch_colmean(const float* x, float* out, int rows, int d, hipStream_t s) {
+  CK_REQUIRE(x && out && rows > 0 && d > 0, "colmean: bad arguments");
+  CK_REQUIRE(d % COLMEAN_COLS == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0,
+             "colmean: d must be a multiple of 32 and x 16-byte aligned");
+  hipLaunchKernelGGL(colmean_kernel, dim3(d / COLMEAN_COLS), dim3(256), 0, s, x, out, rows, d);
   CK_LAUNCHED("colmean");
 }
 
