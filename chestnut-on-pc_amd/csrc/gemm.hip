@@ -309,15 +309,17 @@ __device__ __forceinline__ void lds_barrier() {
 }
 
 // Issue one K-step's loads of this wave into LDS stage `st` (A rows then B rows).
+// ko: the K-step's offset in A (halves); bko: in B (ko for a [N][K] B, ko
+// rows of ldb for a [K][N] B).
 template <int NIA, int NIB, int STAGE_A>
 __device__ __forceinline__ void dma_issue(const half_t* const* asrc, const half_t* const* bsrc, half_t* st, int wave,
-                                          int ko) {
+                                          int ko, long bko) {
 #pragma unroll
   for (int i = 0; i < NIA; ++i)
     __builtin_amdgcn_global_load_lds(asrc[i] + ko, (lds_ptr_t)(st + (wave * NIA + i) * 8 * BK), 16, 0, 0);
 #pragma unroll
   for (int i = 0; i < NIB; ++i)
-    __builtin_amdgcn_global_load_lds(bsrc[i] + ko, (lds_ptr_t)(st + STAGE_A + (wave * NIB + i) * 8 * BK), 16, 0,
+    __builtin_amdgcn_global_load_lds(bsrc[i] + bko, (lds_ptr_t)(st + STAGE_A + (wave * NIB + i) * 8 * BK), 16, 0,
                                      0);
 }
 
@@ -496,7 +498,7 @@ __device__ __forceinline__ void store_staged(const GemmParams& p, const float16_
 // rows); lo and hi are compile-time after unrolling, so the untaken ones vanish.
 template <int NIA, int NIB, int STAGE_A>
 __device__ __forceinline__ void dma_issue_range(const half_t* const* asrc, const half_t* const* bsrc, half_t* st,
-                                                int wave, int ko, int lo, int hi) {
+                                                int wave, int ko, long bko, int lo, int hi) {
 #pragma unroll
   for (int i = 0; i < NIA; ++i)
     if (i >= lo && i < hi)
@@ -504,9 +506,16 @@ __device__ __forceinline__ void dma_issue_range(const half_t* const* asrc, const
 #pragma unroll
   for (int i = 0; i < NIB; ++i)
     if (NIA + i >= lo && NIA + i < hi)
-      __builtin_amdgcn_global_load_lds(bsrc[i] + ko, (lds_ptr_t)(st + STAGE_A + (wave * NIB + i) * 8 * BK), 16, 0,
+      __builtin_amdgcn_global_load_lds(bsrc[i] + bko, (lds_ptr_t)(st + STAGE_A + (wave * NIB + i) * 8 * BK), 16, 0,
                                        0);
 }
+
+// Swizzle of a [K][N] B stage (rows of 128 halves = 16 chunks of 16 bytes):
+// physical chunk = logical chunk ^ bt_swz(row).  The 64 lanes of one
+// transposed fragment read cover rows r0..r0+3 and r0+8..r0+11 (r0 a multiple
+// of 4) x 4 chunks; the swizzle sends them to 16 distinct chunks, two lanes'
+// 8 bytes per chunk, the fewest passes 512 bytes take.
+__device__ __forceinline__ int bt_swz(int row) { return ((row & 3) << 2) | ((row >> 3) & 1); }
 
 // KG K-groups of NWG waves each (64*NWG*KG threads): group g consumes
 // K-steps g, g+KG, g+2KG, ... through its own S/KG stages of the ring, so
@@ -517,7 +526,15 @@ __device__ __forceinline__ void dma_issue_range(const half_t* const* asrc, const
 // every wave the same 64x64 sub-tile as NWG = 4 with 128 rows, while the CU
 // holds two waves per SIMD and each byte it loads feeds twice the MFMAs
 // along M.
-template <int BM, int BN, int S, int KG, int EPI, int NWG = 4>
+// BT: B is [K][N] (N contiguous, config 1's layout).  Its stage holds
+// B[k][n0 .. n0+127] rows (each DMA instruction fills 4 rows x 256 bytes),
+// and the MFMA B fragments come out of LDS transposed by
+// ds_read_b64_tr_b16: within a 16-lane group, source lane 4a+b reads 4
+// halves (n 4b..4b+3) of row a, and lane j receives element j%4 of source
+// lanes 4e + j/4, e = 0..3, i.e. rows 0..3 of column j.  Two such reads give
+// a lane the 8 consecutive k of its column.  Only 128x128 tiles with the f32
+// epilogue take this form.
+template <int BM, int BN, int S, int KG, int EPI, int NWG = 4, bool BT = false>
 __global__ __launch_bounds__(64 * NWG * KG) void gemm_dma_kernel(const GemmParams p) {
   constexpr int STAGE_A = BM * BK, STAGE_B = BN * BK, STAGE = STAGE_A + STAGE_B;   // halves
   static_assert(S % KG == 0 && S / KG >= 2, "each K-group owns at least two ring stages");
@@ -558,10 +575,17 @@ __global__ __launch_bounds__(64 * NWG * KG) void gemm_dma_kernel(const GemmParam
   }
 #pragma unroll
   for (int i = 0; i < NIB; ++i) {
-    const int r = (w4 * NIB + i) * 8 + (lane >> 3);
-    const int q = (lane & 7) ^ ((r >> 1) & 7);
-    bsrc[i] = p.B + bz * p.sB + (long)min(n0 + r, p.N - 1) * p.ldb + kbeg + q * 8;
+    if (BT) {   // instruction i: stage rows (k) 4*(w4*NIB+i) .. +3, lane -> row +lane/16, physical chunk lane%16
+      const int r = (w4 * NIB + i) * 4 + (lane >> 4);
+      const int q = (lane & 15) ^ bt_swz(r);
+      bsrc[i] = p.B + bz * p.sB + (long)(kbeg + r) * p.ldb + n0 + q * 8;
+    } else {
+      const int r = (w4 * NIB + i) * 8 + (lane >> 3);
+      const int q = (lane & 7) ^ ((r >> 1) & 7);
+      bsrc[i] = p.B + bz * p.sB + (long)min(n0 + r, p.N - 1) * p.ldb + kbeg + q * 8;
+    }
   }
+  static_assert(!BT || (BN == 128 && EPI == EPI_F32), "[K][N] B: 128-wide N tiles and the f32 epilogue only");
   float16_t acc[FM][FN];
 #pragma unroll
   for (int i = 0; i < FM; ++i)
@@ -583,7 +607,9 @@ __global__ __launch_bounds__(64 * NWG * KG) void gemm_dma_kernel(const GemmParam
   // group step t is global step KG*t + grp, held in ring stage (KG*t + grp) % S
 #pragma unroll
   for (int t = 0; t < P; ++t)
-    if (t < nkg) dma_issue<NIA, NIB, STAGE_A>(asrc, bsrc, lds + (KG * t + grp) * STAGE, w4, (KG * t + grp) * BK);
+    if (t < nkg)
+      dma_issue<NIA, NIB, STAGE_A>(asrc, bsrc, lds + (KG * t + grp) * STAGE, w4, (KG * t + grp) * BK,
+                                   BT ? (long)(KG * t + grp) * BK * p.ldb : (long)(KG * t + grp) * BK);
 
   int aoff[FM], boff[FN];
 #pragma unroll
@@ -591,6 +617,23 @@ __global__ __launch_bounds__(64 * NWG * KG) void gemm_dma_kernel(const GemmParam
 #pragma unroll
   for (int j = 0; j < FN; ++j) boff[j] = (wn * WN + j * 32 + (lane & 31)) * BK;
   const int rsw = (lane >> 1) & 7;   // ((row >> 1) & 7) of every fragment row this lane reads
+  // [K][N] B: lane (g = lane/16, a = (lane/4)%4, b = lane%4) of a transposed
+  // read of fragment j, k-half h (k = 8*(g/2) + 4h .. +3 of a 16-k slice,
+  // columns 16*(g%2) .. +15 of the fragment) reads row 8*(g/2) + 4h + a of the
+  // slice, halves 4b..4b+3 of the fragment's 16-column block; the row's
+  // swizzle does not depend on the slice (slices are 16 rows).
+  int btoff[FN][2];
+  if (BT) {
+    const int g = lane >> 4, a = (lane >> 2) & 3, b = lane & 3;
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int row = 8 * (g >> 1) + 4 * h + a;
+        const int col = wn * WN + j * 32 + 16 * (g & 1) + 4 * b;
+        btoff[j][h] = row * BN + (((col >> 3) ^ bt_swz(row)) << 3) + (col & 7);
+      }
+  }
 
   for (int t = 0; t < nkg; ++t) {
     const int ahead = min(P - 1, nkg - 1 - t);   // this group's later steps already in flight
@@ -607,6 +650,7 @@ __global__ __launch_bounds__(64 * NWG * KG) void gemm_dma_kernel(const GemmParam
     const bool refill = t + P < nkg;
     half_t* const rst = lds + ((KG * (t + P) + grp) % S) * STAGE;
     const int rko = (KG * (t + P) + grp) * BK;
+    const long rbko = BT ? (long)rko * p.ldb : (long)rko;
     const half_t* sa = lds + ((KG * t + grp) % S) * STAGE;
     const half_t* sb = sa + STAGE_A;
     // Two-deep software pipeline over the step's k-slices, each slice's
@@ -621,14 +665,25 @@ __global__ __launch_bounds__(64 * NWG * KG) void gemm_dma_kernel(const GemmParam
 #pragma unroll
       for (int i = 0; i < FM; ++i) af[kk][i] = *reinterpret_cast<const half8_t*>(sa + aoff[i] + ch);
 #pragma unroll
-      for (int j = 0; j < FN; ++j) bf[kk][j] = *reinterpret_cast<const half8_t*>(sb + boff[j] + ch);
+      for (int j = 0; j < FN; ++j) {
+        if (BT) {
+          typedef short s16x4_t __attribute__((ext_vector_type(4)));
+          typedef __attribute__((address_space(3))) s16x4_t* lds_s4_t;
+          const s16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4_t)(sb + kk * 16 * BN + btoff[j][0]));
+          const s16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4_t)(sb + kk * 16 * BN + btoff[j][1]));
+          const half4_t hl = __builtin_bit_cast(half4_t, lo), hh = __builtin_bit_cast(half4_t, hi);
+          bf[kk][j] = half8_t{hl[0], hl[1], hl[2], hl[3], hh[0], hh[1], hh[2], hh[3]};
+        } else {
+          bf[kk][j] = *reinterpret_cast<const half8_t*>(sb + boff[j] + ch);
+        }
+      }
     };
     read_slice(0);
     read_slice(1);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int kk = 0; kk < KS; ++kk) {
-      if (refill) dma_issue_range<NIA, NIB, STAGE_A>(asrc, bsrc, rst, w4, rko, kk * NI / KS, (kk + 1) * NI / KS);
+      if (refill) dma_issue_range<NIA, NIB, STAGE_A>(asrc, bsrc, rst, w4, rko, rbko, kk * NI / KS, (kk + 1) * NI / KS);
 #pragma unroll
       for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -752,6 +807,14 @@ void launch_dma_tile(const GemmParams& p, bool kg2, hipStream_t s) {
   if (kg2) hipLaunchKernelGGL((gemm_dma_kernel<BM, BN, S2, 2, EPI>), dim3(grid), dim3(512), 0, s, p);
   else hipLaunchKernelGGL((gemm_dma_kernel<BM, BN, S1, 1, EPI>), dim3(grid), dim3(256), 0, s, p);
   CK_LAUNCHED("gemm_dma");
+}
+
+// 128x128 LDS-DMA tile for a [K][N] B (f32 output), two K-groups (tile 1) or one.
+void launch_dma_bt(const GemmParams& p, bool kg2, hipStream_t s) {
+  const int grid = p.Mt * p.Nt * p.split * p.batch;
+  if (kg2) hipLaunchKernelGGL((gemm_dma_kernel<128, 128, 4, 2, EPI_F32, 4, true>), dim3(grid), dim3(512), 0, s, p);
+  else hipLaunchKernelGGL((gemm_dma_kernel<128, 128, 5, 1, EPI_F32, 4, true>), dim3(grid), dim3(256), 0, s, p);
+  CK_LAUNCHED("gemm_dma_bt");
 }
 
 // 256x128 tile: 8 waves of 64x64, one K-group, 3-stage ring (3 x 48 KB).
@@ -912,6 +975,16 @@ void launch_gemm(GemmDesc d, hipStream_t s) {
   }
   if (d.b_kn && !tile_dma(d.tile)) {
     launch_epi<true, EPI_F32>(d.tile, p, s);
+    if (d.split > 1) launch_reduce<EPI_F32>(p, s);
+    return;
+  }
+  if (d.b_kn && d.tile == 1 && p.kps % (2 * BK) == 0 && d.N % 128 == 0 &&
+      (reinterpret_cast<uintptr_t>(d.B) & 15) == 0) {
+    // the [K][N] B straight into LDS, fragments read transposed (no transpose
+    // pass).  Only with two K-groups: on one (tile 5) the doubled fragment
+    // reads cost more than the transpose pass saves (config 1: 44.6 against
+    // 33.2 us; two K-groups 32.6 against 34.9 us).
+    launch_dma_bt(p, true, s);
     if (d.split > 1) launch_reduce<EPI_F32>(p, s);
     return;
   }
