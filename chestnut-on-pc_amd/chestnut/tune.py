@@ -35,15 +35,17 @@ TILES = {1: (128, 128), 2: (128, 64), 3: (64, 128), 4: (64, 64), 5: (128, 128), 
 def shapes(sp):
     """family -> (M, N, K, epilogue kind, batch).  Kinds: 'frag' (QKV fragment
     epilogue, split 1), 'partials' (split-K partials read by the next LN),
-    'f16' (fused activation, split 1), 'reduce' (split allowed, summed by the
-    split-K reduce kernel)."""
+    'f16' (fused activation, split 1), 'conv' (implicit-conv stem layer:
+    split allowed, LDS-DMA tiles 1-8 only), 'reduce' (split allowed, summed
+    by the split-K reduce kernel)."""
     T, d, F = sp['stem'][-1], sp['d_model'], sp['d_ff']
     out = {'qkv': (T, 3 * d, d, 'frag', 1), 'o': (T, d, d, 'partials', 1), 'up': (T, F, d, 'f16', 1),
            'down': (T, d, F, 'partials', 1)}
     H, W, C = sp['img_h'], sp['img_w'], 6 * sp['n_frames']
     for i, co in enumerate(sp['stem']):
         H, W = (H - 1) // 2 + 1, (W - 1) // 2 + 1
-        out[f'stem{i}'] = (H * W, co, -(-9 * C // 64) * 64, 'reduce', 2)
+        # layers after the first run as implicit-conv GEMMs (LDS-DMA tiles 1-8)
+        out[f'stem{i}'] = (H * W, co, -(-9 * C // 64) * 64, 'reduce' if i == 0 else 'conv', 2)
         C = co
     n_spatial = (sp['img_h'] >> len(sp['stem'])) * (sp['img_w'] >> len(sp['stem']))
     out['embed'] = (T, d, 2 * n_spatial, 'reduce', 1)
@@ -67,10 +69,10 @@ def candidates(M, N, K, kind, batch=1, min_wg=64, max_wg=1024):
     for t, (bm, bn) in TILES.items():
         if kind == 'frag' and (N % bn or M % 32):
             continue
-        if t == 9 and kind == 'frag':
+        if t == 9 and kind in ('frag', 'conv'):
             continue
         for s in range(1, 17):
-            if s > 1 and kind not in ('partials', 'reduce'):
+            if s > 1 and kind not in ('partials', 'reduce', 'conv'):
                 continue
             if K % (64 * s) or (s > 1 and K // (64 * s) < 2):
                 continue

@@ -336,6 +336,7 @@ void ck_engine::build_activations() {
     H = Ho; W = Wo; C = sp.stem[i];
   }
   add_tensor("patches", patches * 2, DT_F16, false);
+  add_tensor("zero16", 256, DT_F16, false);   // never written: the implicit conv's border and K-padding source
   add_tensor("tokens", (long)T * 2 * n_spatial * 2, DT_F16, false);
   add_tensor("ctx", (long)d * 4, DT_F32, false);
   add_tensor("x", (long)T * d * 4, DT_F32, false);
@@ -372,7 +373,9 @@ int ck_engine::add_gemm(const std::string& name, const std::string& kernel, Gemm
   ws_floats = std::max(ws_floats, need);
   const double M = g.M, N = g.N, K = g.K, B = g.batch;
   const bool out32 = g.epi == EPI_F32 || g.epi == EPI_F32_RESID;
-  double bytes = B * (M * K + N * K) * 2 + B * M * N * (out32 ? 4 : 2) + (g.bias ? B * N * 4 : 0);
+  // A of an implicit conv: the input activation, each element read once
+  const double a_elems = g.conv_c > 0 ? (double)g.conv_h * g.conv_w * g.conv_c : M * K;
+  double bytes = B * (a_elems + N * K) * 2 + B * M * N * (out32 ? 4 : 2) + (g.bias ? B * N * 4 : 0);
   if (g.epi == EPI_F32_RESID) bytes += B * M * N * 4;
   std::string kern = kernel + (g.split > 1 ? "+splitk" + std::to_string(g.split) : "");
   ck_engine* self = this;
@@ -410,7 +413,11 @@ void ck_engine::build_plan() {
       launch_policy_inputs(q, warped, packed, counter, ring, fr, dr, img, fb, tail, s);
     });
   }
-  // 2. conv stem: im2col with zero-border image reads + MFMA GEMM, both streams batched
+  // 2. conv stem, both streams batched.  Layer 0 (u8 image, 12 channels):
+  // im2col with zero-border image reads + MFMA GEMM.  Later layers (f16,
+  // power-of-two channels): implicit GEMM, the conv GEMM gathers its A chunks
+  // from the previous layer's output (no patch matrix, no im2col launch),
+  // unless the spec pins the layer to a tile without that A path.
   {
     int H = sp.img_h, W = sp.img_w, C = 6 * sp.n_frames;
     for (size_t i = 0; i < sp.stem.size(); ++i) {
@@ -420,6 +427,22 @@ void ck_engine::build_plan() {
       const int Kp = (int)round_up(9L * C, 64);
       half_t* patches = h16("patches");
       const double pbytes = 2.0 * Ho * Wo * Kp * 2;
+      int tile = 0;
+      for (const auto& c : sp.gemm_cfg)
+        if (c.first == "stem" + si + ".conv") tile = c.second.first;
+      const bool implicit = i > 0 && C >= 8 && (C & (C - 1)) == 0 && tile <= 8;
+      if (implicit) {
+        GemmDesc g;
+        g.A = h16("stem." + std::to_string(i - 1) + ".out"); g.sA = (long)H * W * C;
+        g.conv_c = C; g.conv_h = H; g.conv_w = W; g.zero16 = h16("zero16");
+        g.B = h16("stem." + si + ".w"); g.ldb = Kp; g.sB = (long)Co * Kp;
+        g.C = ptr("stem." + si + ".out"); g.ldc = Co; g.sC = (long)Ho * Wo * Co;
+        g.bias = f32("stem." + si + ".b"); g.sBias = Co;
+        g.M = Ho * Wo; g.N = Co; g.K = Kp; g.batch = 2; g.epi = EPI_F16_BIAS_RELU;
+        add_gemm("stem" + si + ".conv", "gemm_conv_relu_implicit", g);
+        H = Ho; W = Wo; C = Co;
+        continue;
+      }
       if (i == 0) {
         const uint8_t* img = static_cast<uint8_t*>(ptr("img"));
         add("stem0.im2col", "im2col_u8", 0, pbytes + 2.0 * C * HW, [=](hipStream_t s) {

@@ -48,7 +48,21 @@ struct GemmParams {
   int vec;            // 1: shapes/alignment allow the LDS-staged 16-byte epilogue
   const half_t* pos;  // EPI_EMBED
   const float* ctx;   // EPI_EMBED
+  int cc_log2, ch, cw, cwo;   // implicit conv: log2(channels), input height/width, output width
+  const half_t* zero;         // implicit conv: 16 zero bytes
 };
+
+// Implicit 3x3 stride-2 pad-1 convolution: the A chunk (8 halves) of patch
+// row m, columns k .. k+7 (one tap, 8 channels: C >= 8) is input pixel
+// (2*ho - 1 + tap/3, 2*wo - 1 + tap%3), channels k%C .. +7, or zeros outside
+// the image and beyond the 9 taps.  yb/xb: 2*ho - 1, 2*wo - 1 of the row.
+__device__ __forceinline__ const half_t* conv_a_src(const GemmParams& p, const half_t* img, int yb, int xb, int k) {
+  const int tap = k >> p.cc_log2, c = k & ((1 << p.cc_log2) - 1);
+  const int dy = (tap * 11) >> 5;   // tap / 3 for tap < 9
+  const int y = yb + dy, x = xb + tap - 3 * dy;
+  const bool ok = tap < 9 && (unsigned)y < (unsigned)p.ch && (unsigned)x < (unsigned)p.cw;
+  return ok ? img + (((long)y * p.cw + x) << p.cc_log2) + c : p.zero;
+}
 
 template <int EPI>
 __device__ __forceinline__ void epi_store(const GemmParams& p, void* C, const float* bias, int m, int n, float v) {
@@ -534,7 +548,9 @@ __device__ __forceinline__ int bt_swz(int row) { return ((row & 3) << 2) | ((row
 // lanes 4e + j/4, e = 0..3, i.e. rows 0..3 of column j.  Two such reads give
 // a lane the 8 consecutive k of its column.  Only 128x128 tiles with the f32
 // epilogue take this form.
-template <int BM, int BN, int S, int KG, int EPI, int NWG = 4, bool BT = false>
+// CV: A is an implicit convolution (conv_a_src): the A chunk addresses are
+// recomputed for every K-step instead of advancing by the step.
+template <int BM, int BN, int S, int KG, int EPI, int NWG = 4, bool BT = false, bool CV = false>
 __global__ __launch_bounds__(64 * NWG * KG) void gemm_dma_kernel(const GemmParams p) {
   constexpr int STAGE_A = BM * BK, STAGE_B = BN * BK, STAGE = STAGE_A + STAGE_B;   // halves
   static_assert(S % KG == 0 && S / KG >= 2, "each K-group owns at least two ring stages");
@@ -567,12 +583,25 @@ __global__ __launch_bounds__(64 * NWG * KG) void gemm_dma_kernel(const GemmParam
   // physical chunk lane%8 <- logical chunk (lane%8) ^ ((row >> 1) & 7)
   const half_t* asrc[NIA];
   const half_t* bsrc[NIB];
+  int cyb[NIA], cxb[NIA], ckq[NIA];   // implicit conv: 2*ho-1, 2*wo-1, the lane's chunk offset in K
 #pragma unroll
   for (int i = 0; i < NIA; ++i) {
     const int r = (w4 * NIA + i) * 8 + (lane >> 3);
     const int q = (lane & 7) ^ ((r >> 1) & 7);
-    asrc[i] = p.A + bz * p.sA + (long)min(m0 + r, p.M - 1) * p.lda + kbeg + q * 8;
+    if (CV) {
+      const int m = min(m0 + r, p.M - 1), ho = m / p.cwo, wo = m - ho * p.cwo;
+      cyb[i] = 2 * ho - 1; cxb[i] = 2 * wo - 1; ckq[i] = kbeg + q * 8;
+      asrc[i] = nullptr;
+    } else {
+      asrc[i] = p.A + bz * p.sA + (long)min(m0 + r, p.M - 1) * p.lda + kbeg + q * 8;
+    }
   }
+  const half_t* const cimg = p.A + bz * p.sA;
+  // implicit conv: the A chunk pointers of K-step ks (offset ks*BK past kbeg)
+  auto conv_step = [&](const half_t** dst, int ks) {
+#pragma unroll
+    for (int i = 0; i < NIA; ++i) dst[i] = conv_a_src(p, cimg, cyb[i], cxb[i], ckq[i] + ks * BK);
+  };
 #pragma unroll
   for (int i = 0; i < NIB; ++i) {
     if (BT) {   // instruction i: stage rows (k) 4*(w4*NIB+i) .. +3, lane -> row +lane/16, physical chunk lane%16
@@ -607,9 +636,16 @@ __global__ __launch_bounds__(64 * NWG * KG) void gemm_dma_kernel(const GemmParam
   // group step t is global step KG*t + grp, held in ring stage (KG*t + grp) % S
 #pragma unroll
   for (int t = 0; t < P; ++t)
-    if (t < nkg)
-      dma_issue<NIA, NIB, STAGE_A>(asrc, bsrc, lds + (KG * t + grp) * STAGE, w4, (KG * t + grp) * BK,
-                                   BT ? (long)(KG * t + grp) * BK * p.ldb : (long)(KG * t + grp) * BK);
+    if (t < nkg) {
+      const long bko = BT ? (long)(KG * t + grp) * BK * p.ldb : (long)(KG * t + grp) * BK;
+      if (CV) {
+        const half_t* acv[NIA];
+        conv_step(acv, KG * t + grp);
+        dma_issue<NIA, NIB, STAGE_A>(acv, bsrc, lds + (KG * t + grp) * STAGE, w4, 0, bko);
+      } else {
+        dma_issue<NIA, NIB, STAGE_A>(asrc, bsrc, lds + (KG * t + grp) * STAGE, w4, (KG * t + grp) * BK, bko);
+      }
+    }
 
   int aoff[FM], boff[FN];
 #pragma unroll
@@ -651,6 +687,10 @@ __global__ __launch_bounds__(64 * NWG * KG) void gemm_dma_kernel(const GemmParam
     half_t* const rst = lds + ((KG * (t + P) + grp) % S) * STAGE;
     const int rko = (KG * (t + P) + grp) * BK;
     const long rbko = BT ? (long)rko * p.ldb : (long)rko;
+    const half_t* acv[NIA];
+    if (CV && refill) conv_step(acv, KG * (t + P) + grp);
+    const half_t* const* ra = CV ? acv : asrc;
+    const int rako = CV ? 0 : rko;
     const half_t* sa = lds + ((KG * t + grp) % S) * STAGE;
     const half_t* sb = sa + STAGE_A;
     // Two-deep software pipeline over the step's k-slices, each slice's
@@ -683,7 +723,7 @@ __global__ __launch_bounds__(64 * NWG * KG) void gemm_dma_kernel(const GemmParam
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int kk = 0; kk < KS; ++kk) {
-      if (refill) dma_issue_range<NIA, NIB, STAGE_A>(asrc, bsrc, rst, w4, rko, rbko, kk * NI / KS, (kk + 1) * NI / KS);
+      if (refill) dma_issue_range<NIA, NIB, STAGE_A>(ra, bsrc, rst, w4, rako, rbko, kk * NI / KS, (kk + 1) * NI / KS);
 #pragma unroll
       for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -809,6 +849,30 @@ void launch_dma_tile(const GemmParams& p, bool kg2, hipStream_t s) {
   CK_LAUNCHED("gemm_dma");
 }
 
+// LDS-DMA tiles with an implicit-convolution A (tile codes 1-8).
+template <int BM, int BN, int EPI>
+void launch_dma_tile_cv(const GemmParams& p, bool kg2, hipStream_t s) {
+  const int grid = p.Mt * p.Nt * p.split * p.batch;
+  constexpr int stage_bytes = (BM + BN) * BK * 2;
+  constexpr int S1 = (5 * stage_bytes <= 163840) ? 5 : 4;
+  constexpr int S2 = (BM == 64 && BN == 64) ? 4 : (6 * stage_bytes <= 163840 ? 6 : 4);
+  if (kg2) hipLaunchKernelGGL((gemm_dma_kernel<BM, BN, S2, 2, EPI, 4, false, true>), dim3(grid), dim3(512), 0, s, p);
+  else hipLaunchKernelGGL((gemm_dma_kernel<BM, BN, S1, 1, EPI, 4, false, true>), dim3(grid), dim3(256), 0, s, p);
+  CK_LAUNCHED("gemm_dma_conv");
+}
+
+template <int EPI>
+void launch_epi_cv(int tile, const GemmParams& p, hipStream_t s) {
+  const int c = tile % 10;
+  const bool kg2 = c <= 4 && p.kps % (2 * BK) == 0;
+  switch (c > 4 ? c - 4 : c) {
+    case 1: launch_dma_tile_cv<128, 128, EPI>(p, kg2, s); break;
+    case 2: launch_dma_tile_cv<128, 64, EPI>(p, kg2, s); break;
+    case 3: launch_dma_tile_cv<64, 128, EPI>(p, kg2, s); break;
+    default: launch_dma_tile_cv<64, 64, EPI>(p, kg2, s); break;
+  }
+}
+
 // 128x128 LDS-DMA tile for a [K][N] B (f32 output), two K-groups (tile 1) or one.
 void launch_dma_bt(const GemmParams& p, bool kg2, hipStream_t s) {
   const int grid = p.Mt * p.Nt * p.split * p.batch;
@@ -916,7 +980,21 @@ size_t gemm_plan(GemmDesc& d) {
 void launch_gemm(GemmDesc d, hipStream_t s) {
   const size_t need = gemm_plan(d);
   CK_REQUIRE(d.A && d.B && (d.C || d.epi == EPI_PARTIALS), "gemm: null operand");
-  CK_REQUIRE(d.lda >= d.K && d.lda % 8 == 0, "gemm: lda must be >= K and a multiple of 8");
+  const bool conv = d.conv_c > 0;
+  if (conv) {
+    const int Ho = (d.conv_h - 1) / 2 + 1, Wo = (d.conv_w - 1) / 2 + 1;
+    CK_REQUIRE(d.conv_c >= 8 && (d.conv_c & (d.conv_c - 1)) == 0 && d.conv_h > 0 && d.conv_w > 0,
+               "gemm: implicit conv needs a power-of-two channel count >= 8");
+    CK_REQUIRE(d.M == Ho * Wo && d.K == ((9 * d.conv_c + BK - 1) / BK) * BK,
+               "gemm: implicit conv needs M = output pixels, K = 9C rounded up to 64");
+    CK_REQUIRE(d.sA >= (long)d.conv_h * d.conv_w * d.conv_c || d.batch == 1, "gemm: implicit conv batch stride");
+    CK_REQUIRE(d.zero16 && (reinterpret_cast<uintptr_t>(d.zero16) & 15) == 0,
+               "gemm: implicit conv needs 16 zero bytes (16-byte aligned)");
+    CK_REQUIRE(!d.b_kn && tile_dma(d.tile) && d.tile != 9 && d.epi == EPI_F16_BIAS_RELU,
+               "gemm: implicit conv runs on the LDS-DMA tiles 1-8 with the bias+ReLU epilogue");
+  } else {
+    CK_REQUIRE(d.lda >= d.K && d.lda % 8 == 0, "gemm: lda must be >= K and a multiple of 8");
+  }
   if (d.b_kn) {
     CK_REQUIRE(d.ldb >= d.N && d.ldb % 8 == 0 && d.N % 8 == 0, "gemm: [K][N] B needs N, ldb multiples of 8");
     CK_REQUIRE(d.epi == EPI_F32, "gemm: [K][N] B supports the f32 epilogue only");
@@ -933,7 +1011,7 @@ void launch_gemm(GemmDesc d, hipStream_t s) {
   if (d.epi == EPI_QKV || d.epi == EPI_QKV_FRAG)
     CK_REQUIRE(d.vt && d.qk_cols > 0 && d.qk_cols < d.N && d.vt_ld >= d.M, "gemm: bad QKV split");
   if (need) CK_REQUIRE(d.ws && d.ws_floats >= need, "gemm: split-K workspace missing or too small");
-  CK_REQUIRE((long)d.M * d.lda < (1L << 31) * 8, "gemm: A too large");
+  CK_REQUIRE(conv || (long)d.M * d.lda < (1L << 31) * 8, "gemm: A too large");
 
   GemmParams p;
   p.A = d.A; p.B = d.B; p.C = d.C; p.bias = d.bias; p.ws = d.ws; p.vt = d.vt;
@@ -945,6 +1023,9 @@ void launch_gemm(GemmDesc d, hipStream_t s) {
   p.head_dim = d.head_dim;
   p.pos = d.pos;
   p.ctx = d.ctx;
+  p.cc_log2 = conv ? __builtin_ctz(d.conv_c) : 0;
+  p.ch = d.conv_h; p.cw = d.conv_w; p.cwo = conv ? (d.conv_w - 1) / 2 + 1 : 0;
+  p.zero = d.zero16;
   if (d.epi == EPI_EMBED)
     CK_REQUIRE(d.pos && d.ctx && (reinterpret_cast<uintptr_t>(d.pos) & 7) == 0 &&
                    (reinterpret_cast<uintptr_t>(d.ctx) & 15) == 0,
@@ -972,6 +1053,11 @@ void launch_gemm(GemmDesc d, hipStream_t s) {
                "than a wave's columns, M % 32 == 0");
     CK_REQUIRE(d.split == 1 && d.batch == 1 && tile_dma(d.tile) && p.vec,
                "gemm: QKV fragment epilogue needs split 1, batch 1, an LDS-DMA tile and aligned outputs");
+  }
+  if (conv) {
+    launch_epi_cv<EPI_F16_BIAS_RELU>(d.tile, p, s);
+    if (d.split > 1) launch_reduce<EPI_F16_BIAS_RELU>(p, s);
+    return;
   }
   if (d.b_kn && !tile_dma(d.tile)) {
     launch_epi<true, EPI_F32>(d.tile, p, s);

@@ -61,6 +61,13 @@ struct GemmDesc {
   int head_dim = 0;            // EPI_QKV_FRAG only
   const half_t* pos = nullptr; // EPI_EMBED: f16 [M][N] position table (row stride ldc)
   const float* ctx = nullptr;  // EPI_EMBED: f32 [N] added to every row
+  // Implicit 3x3 stride-2 pad-1 convolution (conv_c > 0): A is the input
+  // activation f16 [batch][conv_h][conv_w][conv_c] (sA per batch image), row m
+  // of the virtual patch matrix is output pixel m (M = Ho*Wo), column k =
+  // tap*conv_c + channel (K = round_up(9*conv_c, 64)); border taps and the K
+  // padding read the 16 zero bytes at zero16.  conv_c: a power of two >= 8.
+  int conv_c = 0, conv_h = 0, conv_w = 0;
+  const half_t* zero16 = nullptr;
 };
 // Resolves auto tile/split (writes them back) and returns the workspace the
 // launch needs, in floats.

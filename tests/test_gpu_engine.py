@@ -101,6 +101,31 @@ def test_stem_and_context_trace(tiny):
     assert rel_err(eng.read('ctx', np.float32), tr['ctx']) <= 1e-5
 
 
+# stem layers 1-4 as implicit-conv GEMMs on every LDS-DMA tile (tiny: K = 128,
+# 192, 320, 576 -> one or two K-groups, split 3 on the last), and pinned to
+# the register-staged tile 11, which keeps the im2col + GEMM path
+STEM_CFGS = [{f'stem{i}.conv': [t, 3 if (i == 4 and t % 2 == 0) else 1] for i in range(1, 5)}
+             for t in range(1, 9)] + [{f'stem{i}.conv': [11, 1] for i in range(1, 5)}]
+
+
+@pytest.mark.parametrize('cfg', STEM_CFGS, ids=lambda c: 'tile%d' % c['stem1.conv'][0])
+def test_stem_implicit_conv_tiles(tiny, cfg):
+    sp, w, _ = tiny
+    orc = OM.OracleModel(sp, w)
+    rng = np.random.default_rng(21)
+    warped, packed = next(frame_inputs(rng, sp, 1))
+    orc.run_frame(warped, packed)
+    print(f'[stem] cfg={cfg}', flush=True)
+    eng = Engine(dict(sp, gemm_config=cfg), weights=w)
+    try:
+        eng.run_frame(warped, packed)
+        so = eng.read(f'stem.{len(sp["stem"]) - 1}.out', np.float16).reshape(2, 4, 8, -1).astype(np.float64)
+    finally:
+        eng.close()
+    for s in range(2):
+        assert rel_err(so[s], orc.trace[f'stem{s}']) <= REL, (cfg, s)
+
+
 def test_graph_equals_eager_and_device_loop(tiny):
     sp, w, eng = tiny
     rng = np.random.default_rng(14)

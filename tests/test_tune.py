@@ -31,9 +31,10 @@ def test_stem_and_embed_shapes():
     sp = S.get_spec('big_driving_1b')
     sh = TU.shapes(sp)
     assert sh['stem0'] == (64 * 128, 32, 128, 'reduce', 2)          # 9 x 12 channels padded to 128
-    assert sh['stem4'] == (4 * 8, 512, 9 * 256, 'reduce', 2)
+    assert sh['stem4'] == (4 * 8, 512, 9 * 256, 'conv', 2)          # implicit conv: no tile 9
     assert sh['embed'] == (512, 2048, 64, 'reduce', 1)
     assert TU.entry_names(sp, 'stem3') == ['stem3.conv'] and TU.entry_names(sp, 'embed') == ['embed']
     M, N, K, kind, b = sh['stem4']
     c = TU.candidates(M, N, K, kind, b)
     assert c and all(K % (64 * s) == 0 for _, s in c)
+    assert all(t <= 8 for t, _ in c) and any(s > 1 for _, s in c)
