@@ -431,6 +431,11 @@ void ck_engine::build_plan() {
       for (const auto& c : sp.gemm_cfg)
         if (c.first == "stem" + si + ".conv") tile = c.second.first;
       const bool implicit = i > 0 && C >= 8 && (C & (C - 1)) == 0 && tile <= 8;
+      // default 64x64 tiles; split-K 6 only for the longest K (measured per
+      // layer on the 1B stem over every candidate: 64x64 unsplit is fastest
+      // up to K = 1152, 64x64 split 6 at K = 2304, 0.4-0.9 us ahead of the
+      // automatic choice on each layer)
+      const int stem_split = (Kp / 64 >= 32 && (Kp / 64) % 6 == 0) ? 6 : 1;
       if (implicit) {
         GemmDesc g;
         g.A = h16("stem." + std::to_string(i - 1) + ".out"); g.sA = (long)H * W * C;
@@ -439,6 +444,7 @@ void ck_engine::build_plan() {
         g.C = ptr("stem." + si + ".out"); g.ldc = Co; g.sC = (long)Ho * Wo * Co;
         g.bias = f32("stem." + si + ".b"); g.sBias = Co;
         g.M = Ho * Wo; g.N = Co; g.K = Kp; g.batch = 2; g.epi = EPI_F16_BIAS_RELU;
+        g.tile = 4; g.split = stem_split;
         add_gemm("stem" + si + ".conv", "gemm_conv_relu_implicit", g);
         H = Ho; W = Wo; C = Co;
         continue;
@@ -460,6 +466,7 @@ void ck_engine::build_plan() {
       g.C = ptr("stem." + si + ".out"); g.ldc = Co; g.sC = (long)Ho * Wo * Co;
       g.bias = f32("stem." + si + ".b"); g.sBias = Co;
       g.M = Ho * Wo; g.N = Co; g.K = Kp; g.batch = 2; g.epi = EPI_F16_BIAS_RELU;
+      g.tile = 4; g.split = stem_split;
       add_gemm("stem" + si + ".conv", "gemm_conv_relu", g);
       H = Ho; W = Wo; C = Co;
     }
