@@ -413,6 +413,7 @@ void ck_engine::build_plan() {
       launch_policy_inputs(q, warped, packed, counter, ring, fr, dr, img, fb, tail, s);
     });
   }
+  bool tokens_fused = false;
   // 2. conv stem, both streams batched.  Layer 0 (u8 image, 12 channels):
   // im2col with zero-border image reads + MFMA GEMM.  Later layers (f16,
   // power-of-two channels): implicit GEMM, the conv GEMM gathers its A chunks
@@ -427,9 +428,9 @@ void ck_engine::build_plan() {
       const int Kp = (int)round_up(9L * C, 64);
       half_t* patches = h16("patches");
       const double pbytes = 2.0 * Ho * Wo * Kp * 2;
-      int tile = 0;
+      int tile = 0, cfg_split = -1;
       for (const auto& c : sp.gemm_cfg)
-        if (c.first == "stem" + si + ".conv") tile = c.second.first;
+        if (c.first == "stem" + si + ".conv") { tile = c.second.first; cfg_split = c.second.second; }
       const bool implicit = i > 0 && C >= 8 && (C & (C - 1)) == 0 && tile <= 8;
       // default 64x64 tiles; split-K 6 only for the longest K (measured per
       // layer on the 1B stem over every candidate: 64x64 unsplit is fastest
@@ -445,6 +446,13 @@ void ck_engine::build_plan() {
         g.bias = f32("stem." + si + ".b"); g.sBias = Co;
         g.M = Ho * Wo; g.N = Co; g.K = Kp; g.batch = 2; g.epi = EPI_F16_BIAS_RELU;
         g.tile = 4; g.split = stem_split;
+        // last layer with split-K: its reduce stores the channels-as-tokens
+        // transpose F[c][s*NS + p] directly (no separate tokens launch)
+        const int eff_split = cfg_split >= 0 ? cfg_split : stem_split;
+        if (i + 1 == sp.stem.size() && eff_split > 1 && Co == T && Ho * Wo == n_spatial) {
+          g.c_nm = 1; g.C = ptr("tokens"); g.ldc = 2L * n_spatial; g.sC = n_spatial;
+          tokens_fused = true;
+        }
         add_gemm("stem" + si + ".conv", "gemm_conv_relu_implicit", g);
         H = Ho; W = Wo; C = Co;
         continue;
@@ -476,7 +484,8 @@ void ck_engine::build_plan() {
     const half_t* so = h16("stem." + std::to_string(sp.stem.size() - 1) + ".out");
     half_t* tok = h16("tokens");
     const int ns = n_spatial, C5 = T;
-    add("tokens", "tokens", 0, 2.0 * 2 * ns * C5 * 2, [=](hipStream_t s) { launch_tokens(so, ns, C5, tok, s); });
+    if (!tokens_fused)
+      add("tokens", "tokens", 0, 2.0 * 2 * ns * C5 * 2, [=](hipStream_t s) { launch_tokens(so, ns, C5, tok, s); });
     const int Kt = sp.feat_hist * sp.feat_len, Td = sp.temporal_dim;
     const half_t* tw = h16("tmp.w");
     const float* tb = f32("tmp.b");

@@ -50,6 +50,7 @@ struct GemmParams {
   const float* ctx;   // EPI_EMBED
   int cc_log2, ch, cw, cwo;   // implicit conv: log2(channels), input height/width, output width
   const half_t* zero;         // implicit conv: 16 zero bytes
+  int c_nm;                   // the split-K reduce stores element (m, n) at C[n*ldc + m]
 };
 
 // Implicit 3x3 stride-2 pad-1 convolution: the A chunk (8 halves) of patch
@@ -84,6 +85,8 @@ __device__ __forceinline__ void epi_store(const GemmParams& p, void* C, const fl
       return;   // unreachable: the host admits EPI_QKV_FRAG only with the staged epilogue
     } else if (EPI == EPI_QKV && n >= p.qk_cols) {
       p.vt[(long)(n - p.qk_cols) * p.vt_ld + m] = (half_t)v;
+    } else if (p.c_nm) {
+      static_cast<half_t*>(C)[(long)n * p.ldc + m] = (half_t)v;
     } else {
       static_cast<half_t*>(C)[(long)m * p.ldc + n] = (half_t)v;
     }
@@ -1003,8 +1006,8 @@ void launch_gemm(GemmDesc d, hipStream_t s) {
   }
   // QKV: only the first qk_cols columns are stored row-major in C
   if (d.epi != EPI_PARTIALS)
-    CK_REQUIRE(d.ldc >= ((d.epi == EPI_QKV || d.epi == EPI_QKV_FRAG) ? d.qk_cols : d.N),
-               "gemm: ldc must be >= N (>= qk_cols for QKV)");
+    CK_REQUIRE(d.ldc >= (d.c_nm ? d.M : (d.epi == EPI_QKV || d.epi == EPI_QKV_FRAG) ? d.qk_cols : d.N),
+               "gemm: ldc must be >= N (>= qk_cols for QKV, >= M for a transposed store)");
   CK_REQUIRE((reinterpret_cast<uintptr_t>(d.A) & 15) == 0 && (reinterpret_cast<uintptr_t>(d.B) & 15) == 0,
              "gemm: A and B must be 16-byte aligned");
   CK_REQUIRE(d.sA % 8 == 0 && d.sB % 8 == 0, "gemm: batch strides must keep 16-byte alignment");
@@ -1026,6 +1029,9 @@ void launch_gemm(GemmDesc d, hipStream_t s) {
   p.cc_log2 = conv ? __builtin_ctz(d.conv_c) : 0;
   p.ch = d.conv_h; p.cw = d.conv_w; p.cwo = conv ? (d.conv_w - 1) / 2 + 1 : 0;
   p.zero = d.zero16;
+  CK_REQUIRE(!d.c_nm || (d.split > 1 && d.epi == EPI_F16_BIAS_RELU && d.tile <= 8),
+             "gemm: a transposed C store is done by the split-K reduce of the bias+ReLU epilogue only");
+  p.c_nm = d.c_nm;
   if (d.epi == EPI_EMBED)
     CK_REQUIRE(d.pos && d.ctx && (reinterpret_cast<uintptr_t>(d.pos) & 7) == 0 &&
                    (reinterpret_cast<uintptr_t>(d.ctx) & 15) == 0,

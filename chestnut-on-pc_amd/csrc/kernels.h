@@ -68,6 +68,9 @@ struct GemmDesc {
   // padding read the 16 zero bytes at zero16.  conv_c: a power of two >= 8.
   int conv_c = 0, conv_h = 0, conv_w = 0;
   const half_t* zero16 = nullptr;
+  // Store the f16 result transposed, C[b*sC + n*ldc + m] (the split-K
+  // reduce of EPI_F16_BIAS_RELU on tiles 1-8 only; requires split > 1).
+  int c_nm = 0;
 };
 // Resolves auto tile/split (writes them back) and returns the workspace the
 // launch needs, in floats.

@@ -102,8 +102,9 @@ def test_stem_and_context_trace(tiny):
 
 
 # stem layers 1-4 as implicit-conv GEMMs on every LDS-DMA tile (tiny: K = 128,
-# 192, 320, 576 -> one or two K-groups, split 3 on the last), and pinned to
-# the register-staged tile 11, which keeps the im2col + GEMM path
+# 192, 320, 576 -> one or two K-groups, split 3 on the last, whose reduce then
+# writes the tokens), and pinned to the register-staged tile 11, which keeps
+# the im2col + GEMM path
 STEM_CFGS = [{f'stem{i}.conv': [t, 3 if (i == 4 and t % 2 == 0) else 1] for i in range(1, 5)}
              for t in range(1, 9)] + [{f'stem{i}.conv': [11, 1] for i in range(1, 5)}]
 
@@ -120,9 +121,15 @@ def test_stem_implicit_conv_tiles(tiny, cfg):
     try:
         eng.run_frame(warped, packed)
         so = eng.read(f'stem.{len(sp["stem"]) - 1}.out', np.float16).reshape(2, 4, 8, -1).astype(np.float64)
+        tok = eng.read('tokens', np.float16, orc.trace['tokens'].shape).astype(np.float64)
+        fused = 'tokens' not in [e['name'] for e in eng.plan()]
     finally:
         eng.close()
-    for s in range(2):
+    # a split last layer stores the tokens transpose from its reduce and
+    # leaves stem.4.out unwritten
+    assert fused == (cfg['stem4.conv'][1] > 1)
+    assert rel_err(tok, orc.trace['tokens']) <= REL, cfg
+    for s in range(2 if not fused else 0):
         assert rel_err(so[s], orc.trace[f'stem{s}']) <= REL, (cfg, s)
 
 
