@@ -432,11 +432,15 @@ void ck_engine::build_plan() {
       for (const auto& c : sp.gemm_cfg)
         if (c.first == "stem" + si + ".conv") { tile = c.second.first; cfg_split = c.second.second; }
       const bool implicit = i > 0 && C >= 8 && (C & (C - 1)) == 0 && tile <= 8;
-      // default 64x64 tiles; split-K 6 only for the longest K (measured per
-      // layer on the 1B stem over every candidate: 64x64 unsplit is fastest
-      // up to K = 1152, 64x64 split 6 at K = 2304, 0.4-0.9 us ahead of the
-      // automatic choice on each layer)
-      const int stem_split = (Kp / 64 >= 32 && (Kp / 64) % 6 == 0) ? 6 : 1;
+      // default 64x64 tiles (one K-group for the implicit layers), and for
+      // 18 or more K-steps a split that leaves 3 steps per workgroup: chosen
+      // on whole 1B frames over every candidate (python -m chestnut.tune),
+      // where the stem's weights arrive cold and a few long K chains are
+      // latency-bound (K = 1152: split 6, K = 2304: split 12, -0.9% per frame
+      // over unsplit two-K-group tiles)
+      const int ksteps = Kp / 64;
+      const int stem_split = (ksteps >= 18 && ksteps % 3 == 0) ? std::min(16, ksteps / 3) : 1;
+      const int stem_tile = i == 0 ? 4 : 8;
       if (implicit) {
         GemmDesc g;
         g.A = h16("stem." + std::to_string(i - 1) + ".out"); g.sA = (long)H * W * C;
@@ -445,7 +449,7 @@ void ck_engine::build_plan() {
         g.C = ptr("stem." + si + ".out"); g.ldc = Co; g.sC = (long)Ho * Wo * Co;
         g.bias = f32("stem." + si + ".b"); g.sBias = Co;
         g.M = Ho * Wo; g.N = Co; g.K = Kp; g.batch = 2; g.epi = EPI_F16_BIAS_RELU;
-        g.tile = 4; g.split = stem_split;
+        g.tile = stem_tile; g.split = stem_split;
         // last layer with split-K: its reduce stores the channels-as-tokens
         // transpose F[c][s*NS + p] directly (no separate tokens launch)
         const int eff_split = cfg_split >= 0 ? cfg_split : stem_split;
@@ -474,7 +478,7 @@ void ck_engine::build_plan() {
       g.C = ptr("stem." + si + ".out"); g.ldc = Co; g.sC = (long)Ho * Wo * Co;
       g.bias = f32("stem." + si + ".b"); g.sBias = Co;
       g.M = Ho * Wo; g.N = Co; g.K = Kp; g.batch = 2; g.epi = EPI_F16_BIAS_RELU;
-      g.tile = 4; g.split = stem_split;
+      g.tile = stem_tile; g.split = stem_split;
       add_gemm("stem" + si + ".conv", "gemm_conv_relu", g);
       H = Ho; W = Wo; C = Co;
     }
