@@ -436,8 +436,8 @@ void ck_engine::build_plan() {
       // 18 or more K-steps a split that leaves 3 steps per workgroup: chosen
       // on whole 1B frames over every candidate (python -m chestnut.tune),
       // where the stem's weights arrive cold and a few long K chains are
-      // latency-bound (K = 1152: split 6, K = 2304: split 12, -0.9% per frame
-      // over unsplit two-K-group tiles)
+      // latency-bound (K = 1152: split 6, K = 2304: split 12, -0.45% per
+      // frame over unsplit two-K-group tiles)
       const int ksteps = Kp / 64;
       const int stem_split = (ksteps >= 18 && ksteps % 3 == 0) ? std::min(16, ksteps / 3) : 1;
       const int stem_tile = i == 0 ? 4 : 8;

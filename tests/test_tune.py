@@ -12,6 +12,7 @@ def test_candidates_respect_epilogue_and_grid():
     M, N, K, kind, _ = sh['o']
     c = TU.candidates(M, N, K, kind)
     assert (2, 2) in c and (1, 4) in c and (4, 1) in c
+    assert all(s <= 8 for _, s in c)                                       # the LayerNorm sums <= 8 partials
     for t, s in c:
         bm, bn = TU.TILES[t]
         grid = -(-M // bm) * -(-N // bn) * s
