@@ -66,21 +66,62 @@ __global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(const GemvArgs a0, c
   const half_t* __restrict__ W = a.W;
   const int rows = a.rows, K = a.K, ldw = a.ldw;
 
+  const int r0 = blk * a.rows_per_wg;
+  const int r1 = min(rows, r0 + a.rows_per_wg);
+  // W batch loads: RB rows x NSTEP 16-byte chunks per lane.  With the
+  // GRU-gated input the first batch is issued before the gates are
+  // evaluated, so its latency overlaps that work; the plain form loads each
+  // batch at the top of its iteration (an early load there costs registers
+  // and occupancy on the wide GEMVs).
+  half8_t w[GEMV_RB][NSTEP];
+  auto load_batch = [&](int rb) {
+#pragma unroll
+    for (int i = 0; i < GEMV_RB; ++i) {
+      const int r = min(rb + i, r1 - 1);   // tail rows re-read the last row; their sums are dropped
+      const half_t* wr = W + (long)r * ldw;
+#pragma unroll
+      for (int s = 0; s < NSTEP; ++s) {
+        const int c = s * GEMV_STEP_COLS + t * 8;
+        if (GATE) {
+          // columns past K re-read the row's last chunk (in bounds, finite)
+          // and meet x = 0, adding exact zeros: without a branch the gate
+          // loads and arithmetic need not wait for these loads
+          w[i][s] = __builtin_nontemporal_load(reinterpret_cast<const half8_t*>(wr + min(c, K - 8)));
+        } else if (c < K) {
+          // the branch keeps every load of the batch ahead of the first FMA
+          // (branch-free, the compiler interleaves loads with the FMAs and
+          // holds about 2 in flight per lane instead of RB*NSTEP)
+          w[i][s] = __builtin_nontemporal_load(reinterpret_cast<const half8_t*>(wr + c));
+        } else {
+          w[i][s] = half8_t{};
+        }
+      }
+    }
+  };
+  if (GATE && r0 < r1) load_batch(r0);
+
   float xr[NSTEP][8];
-  bool cv[NSTEP];
 #pragma unroll
   for (int s = 0; s < NSTEP; ++s) {
     const int c = s * GEMV_STEP_COLS + t * 8;
-    cv[s] = c < K;
-    if (cv[s]) {
+    if (c < K) {
       if (GATE) {
+        // all seven 8-float slices are loaded before any gate is evaluated
+        const float* src[7] = {a.gi + c, a.gi + K + c, a.gi + 2 * K + c, a.gh + c, a.gh + K + c, a.gh + 2 * K + c,
+                               a.hp + c};
+        float4_t g[7][2];
+#pragma unroll
+        for (int q = 0; q < 7; ++q) {
+          g[q][0] = *reinterpret_cast<const float4_t*>(src[q]);
+          g[q][1] = *reinterpret_cast<const float4_t*>(src[q] + 4);
+        }
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-          const int cj = c + j;
-          const float r = sigmoidf_(a.gi[cj] + a.gh[cj]);
-          const float z = sigmoidf_(a.gi[K + cj] + a.gh[K + cj]);
-          const float n = tanhf(a.gi[2 * K + cj] + r * a.gh[2 * K + cj]);
-          xr[s][j] = (1.0f - z) * n + z * a.hp[cj];
+          const int h = j >> 2, e = j & 3;
+          const float r = sigmoidf_(g[0][h][e] + g[3][h][e]);
+          const float z = sigmoidf_(g[1][h][e] + g[4][h][e]);
+          const float n = tanhf(g[2][h][e] + r * g[5][h][e]);
+          xr[s][j] = (1.0f - z) * n + z * g[6][h][e];
         }
         if (blk == 0) {
 #pragma unroll
@@ -101,22 +142,10 @@ __global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(const GemvArgs a0, c
     }
   }
 
-  const int r0 = blk * a.rows_per_wg;
-  const int r1 = min(rows, r0 + a.rows_per_wg);
   int par = 0;
   for (int rb = r0; rb < r1; rb += GEMV_RB, par ^= 1) {
-    half8_t w[GEMV_RB][NSTEP];
-#pragma unroll
-    for (int i = 0; i < GEMV_RB; ++i) {
-      const int r = min(rb + i, r1 - 1);   // tail rows re-read the last row; their sums are dropped
-      const half_t* wr = W + (long)r * ldw + t * 8;
-#pragma unroll
-      for (int s = 0; s < NSTEP; ++s) {
-        if (cv[s]) w[i][s] = __builtin_nontemporal_load(reinterpret_cast<const half8_t*>(wr + s * GEMV_STEP_COLS));
-        else w[i][s] = half8_t{};
-      }
-    }
-    float acc[GEMV_RB];
+    if (!GATE || rb != r0) load_batch(rb);
+    float part[GEMV_RB];
 #pragma unroll
     for (int i = 0; i < GEMV_RB; ++i) {
       float v = 0.f;
@@ -124,8 +153,11 @@ __global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(const GemvArgs a0, c
       for (int s = 0; s < NSTEP; ++s)
 #pragma unroll
         for (int j = 0; j < 8; ++j) v = fmaf((float)w[i][s][j], xr[s][j], v);
-      acc[i] = wave_sum(v);
+      part[i] = v;
     }
+    float acc[GEMV_RB];
+#pragma unroll
+    for (int i = 0; i < GEMV_RB; ++i) acc[i] = wave_sum(part[i]);
     if (lane == 0) {
 #pragma unroll
       for (int i = 0; i < GEMV_RB; ++i) red[par][wave][i] = acc[i];
@@ -159,6 +191,9 @@ void check_args(const GemvArgs& a) {
   CK_REQUIRE((reinterpret_cast<uintptr_t>(a.W) & 15) == 0 && (reinterpret_cast<uintptr_t>(a.x) & 15) == 0,
              "gemv: W and x must be 16-byte aligned");
   CK_REQUIRE(!a.gi || (a.gh && a.hp && a.h1), "gemv: the GRU-gated input needs gi, gh, h_prev and an output for h");
+  CK_REQUIRE(!a.gi || ((reinterpret_cast<uintptr_t>(a.gi) | reinterpret_cast<uintptr_t>(a.gh) |
+                        reinterpret_cast<uintptr_t>(a.hp)) & 15) == 0,
+             "gemv: gi, gh and h_prev must be 16-byte aligned");
   CK_REQUIRE(a.act == GEMV_NONE || a.act == GEMV_GELU, "gemv: unknown activation");
 }
 
