@@ -4,7 +4,7 @@ on one MI355X, replayed as one hipGraph per frame, plus per-kernel roofline
 fractions and the CPU oracle timed on the same host.
 
     python bench.py [--gpus 1] [--steps 50] [--warmup 5] [--spec big_driving_1b]
-                    [--cpu-frames 3] [--no-cpu] [--no-micro]
+                    [--cpu-reps 5] [--no-cpu] [--no-micro]
                     [--dump-plan PATH] [--pmc-run FAMILY [--pmc-reps N] [--pmc-out PATH]]
 
 A step is one frame: inputs (uint8 frame pair + packed f32 vector) already
@@ -183,28 +183,47 @@ def traffic_record(spec_name, fam):
     return None
 
 
-def cpu_baseline(sp, weights, n_frames, warped, packed):
-    """The numpy oracle (f32 OpenBLAS) on this host's cores, bounded sample."""
-    from threadpoolctl import threadpool_limits
+def cpu_baseline(sp, weights, warped, packed, reps=5):
+    """The numpy oracle (f32 OpenBLAS) on this host's cores, bounded sample:
+    one warm-up frame, then `reps` timed frames (the recurrent loop, hidden
+    state fed back), reported as the median frame rate.
+
+    Threads: every core of the process's affinity mask, capped by the CPU
+    share the host grants one GPU's job when it states one (OMP_NUM_THREADS,
+    16 on the GPU boxes), exported as OPENBLAS_NUM_THREADS and applied to the
+    loaded BLAS with threadpoolctl."""
+    from threadpoolctl import threadpool_info, threadpool_limits
     from oracle.model import OracleModel
-    cores = min(16, len(os.sched_getaffinity(0)))
+    affinity = len(os.sched_getaffinity(0))
+    share = int(os.environ.get('OMP_NUM_THREADS', '0') or 0)
+    cores = min(affinity, share) if share > 0 else affinity
+    os.environ['OPENBLAS_NUM_THREADS'] = str(cores)
     with threadpool_limits(limits=cores):
+        blas = [f"{i.get('internal_api')}x{i.get('num_threads')}" for i in threadpool_info()
+                if i.get('user_api') == 'blas']
         orc = OracleModel(sp, weights, acc=np.float32)
-        t0 = time.perf_counter()
         pk = packed.copy()
-        for _ in range(n_frames):
+        o = orc.run_frame(warped, pk)            # warm-up frame (first-touch of the f32 weights)
+        pk[12:] = o[-sp['hidden']:]
+        ts = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
             o = orc.run_frame(warped, pk)
+            ts.append(time.perf_counter() - t0)
             pk[12:] = o[-sp['hidden']:]
-        dt = time.perf_counter() - t0
     cpu = ''
     try:
         with open('/proc/cpuinfo') as fh:
             cpu = next((l.split(':', 1)[1].strip() for l in fh if l.startswith('model name')), '')
     except OSError:
         pass
-    return {'value': round(n_frames / dt, 4), 'unit': 'frames/s', 'cores': cores, 'kind': 'port',
-            'sample': f'{n_frames} frame(s) of {sp["name"]} through oracle/model.py (numpy f32, OpenBLAS), '
-                      f'{dt:.1f} s; host CPU: {cpu}'}
+    med = float(np.median(ts))
+    return {'value': round(1.0 / med, 4), 'unit': 'frames/s', 'cores': cores, 'kind': 'port',
+            'affinity_cores': affinity, 'cpu_model': cpu, 'blas': blas,
+            'frame_s': {'median': round(med, 3), 'min': round(min(ts), 3), 'max': round(max(ts), 3)},
+            'sample': f'{sp["name"]} through oracle/model.py (numpy f32, OpenBLAS, {cores} threads of '
+                      f'{affinity} in the affinity mask): 1 warm-up frame, then the median of {reps} timed '
+                      f'recurrent frames ({sum(ts):.1f} s); host CPU: {cpu}'}
 
 
 def main():
@@ -213,7 +232,7 @@ def main():
     ap.add_argument('--steps', type=int, default=50)
     ap.add_argument('--warmup', type=int, default=5)
     ap.add_argument('--spec', default='big_driving_1b')
-    ap.add_argument('--cpu-frames', type=int, default=3)
+    ap.add_argument('--cpu-reps', type=int, default=5, help='timed CPU-oracle frames (after one warm-up)')
     ap.add_argument('--no-cpu', action='store_true')
     ap.add_argument('--no-micro', action='store_true')
     ap.add_argument('--dump-plan', default=None, help='write the frame plan (name, kernel, flops, bytes) as JSON')
@@ -354,7 +373,7 @@ def main():
         line['config4'] = config4_fps()
         log(f'[bench] config 4 {line["config4"]}')
     if not a.no_cpu:
-        line['cpu_baseline'] = cpu_baseline(sp, weights, a.cpu_frames, warped, packed)
+        line['cpu_baseline'] = cpu_baseline(sp, weights, warped, packed, a.cpu_reps)
         log(f'[bench] cpu baseline {line["cpu_baseline"]}')
     print(json.dumps(line), flush=True)
 

@@ -9,6 +9,7 @@ returns a namespace with exactly those attributes.
 import ctypes
 import json
 import types
+from collections.abc import Mapping
 from concurrent.futures import ThreadPoolExecutor
 
 import numpy as np
@@ -119,6 +120,7 @@ class Engine:
             raise ValueError(f'warped must be uint8 {(2, 6, s["img_h"], s["img_w"])}, got {w.shape}')
         if p.shape != self.PACKED.shape:
             raise ValueError(f'packed must be f32 {self.PACKED.shape}, got {p.shape}')
+        self.PACKED[:] = p                   # PACKED[:] = packed (run_pinned2.py:1464)
         out = np.empty(self.n_out, np.float32)
         call('ck_run_frame', self._h, w.ctypes.data, p.ctypes.data, out.ctypes.data)
         return out
@@ -267,9 +269,72 @@ class Engine:
             self.write(n, a)
 
 
+class Queues(Mapping):
+    """The reference's `queues` dict (run_pinned2.py:1379-1386), read live
+    from the device rings.
+
+    The engine never shifts its queues: each is a ring indexed by the frame
+    counter (csrc/pack.hip).  Reading a key rebuilds the reference's queue,
+    oldest entry first, from the ring and the counter -- after N frames
+    position j of a length-L queue holds the entry of frame N - L + j (zero
+    for frames before the first), exactly what the reference's shift-by-one
+    queues hold:
+      img_q, big_img_q   uint8 (FS*(n_frames-1)+1, 6, H, W)
+      feat_q             f32 (FS*feat_hist, 1, feat_len)
+      desire_q           f32 (FS*desire_hist, 1, desire_len)
+      packed_npy_inputs  the PACKED staging vector (desire | tc | action_t | prev_feat)
+    Values are host copies taken at the time of the lookup.
+    """
+
+    _KEYS = ('img_q', 'big_img_q', 'feat_q', 'desire_q', 'packed_npy_inputs')
+
+    def __init__(self, eng):
+        self._eng = eng
+
+    def __iter__(self):
+        return iter(self._KEYS)
+
+    def __len__(self):
+        return len(self._KEYS)
+
+    def frames(self):
+        """Frames pushed since the last reset (the device frame counter)."""
+        return int(self._eng.read('counter', np.uint32)[0])
+
+    @staticmethod
+    def _unroll(ring, n):
+        """Reference order of a ring of L entries after n pushes."""
+        L = ring.shape[0]
+        out = np.zeros_like(ring)
+        for j in range(L):
+            f = n - L + j
+            if f >= 0:
+                out[j] = ring[f % L]
+        return out
+
+    def __getitem__(self, key):
+        e, s = self._eng, self._eng.spec
+        if key == 'packed_npy_inputs':
+            return e.PACKED
+        if key not in self._KEYS:
+            raise KeyError(key)
+        fs = s.get('frame_skip', 4)
+        n = self.frames()
+        if key in ('img_q', 'big_img_q'):
+            slots = fs * (s.get('n_frames', 2) - 1) + 1
+            ring = e.read('img_ring', np.uint8, (2, slots, 6, s['img_h'], s['img_w']))
+            return self._unroll(ring[0 if key == 'img_q' else 1], n)
+        if key == 'feat_q':
+            ring = e.read('feat_ring', np.float32, (fs * s['feat_hist'], 1, s['feat_len']))
+            return self._unroll(ring, n)
+        ring = e.read('desire_ring', np.float32, (fs * s['desire_hist'], 1, s['desire_len']))
+        return self._unroll(ring, n)
+
+
 def load(spec='big_driving_1b', **kw):
-    """The reference's exec-prefix namespace (run_pinned2.py:1346-1572):
-    run_frame, out_slices, img, make_warped, PACKED, plus the engine."""
+    """The reference's exec-prefix namespace (run_pinned2.py:1346-1572;
+    video_demo.py:25): run_frame, out_slices, img, make_warped, queues,
+    PACKED, plus the engine."""
     eng = Engine(spec, **kw)
     return types.SimpleNamespace(run_frame=eng.run_frame, out_slices=eng.out_slices, img=eng.img,
-                                 make_warped=eng.make_warped, PACKED=eng.PACKED, engine=eng)
+                                 make_warped=eng.make_warped, queues=Queues(eng), PACKED=eng.PACKED, engine=eng)

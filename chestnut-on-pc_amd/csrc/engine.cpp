@@ -89,6 +89,7 @@ Spec parse_spec(const std::string& json) {
   }
   // structural requirements of the kernels
   CK_REQUIRE(s.n_frames == 2, "spec: n_frames must be 2 (two sampled frames per stream)");
+  CK_REQUIRE(s.fs >= 1, "spec: frame_skip must be >= 1");
   CK_REQUIRE(s.d == s.n_heads * s.head_dim, "spec: d_model must equal n_heads * head_dim");
   CK_REQUIRE(s.hidden == s.feat_len, "spec: hidden must equal feat_len (prev_feat is the GRU state)");
   CK_REQUIRE(s.img_h % (1 << s.stem.size()) == 0 && s.img_w % (1 << s.stem.size()) == 0,
@@ -102,7 +103,19 @@ Spec parse_spec(const std::string& json) {
 
 using namespace ck;
 
+// A failure anywhere in set-up (a rejected gemm_config, an allocation)
+// releases everything allocated so far before the exception leaves: a
+// throwing constructor never runs the destructor.
 ck_engine::ck_engine(const std::string& spec_json) : sp(parse_spec(spec_json)) {
+  try {
+    init();
+  } catch (...) {
+    release();
+    throw;
+  }
+}
+
+void ck_engine::init() {
   T = sp.stem.back();
   n_spatial = (sp.img_h >> sp.stem.size()) * (sp.img_w >> sp.stem.size());
   n_head_out = 0;
@@ -132,11 +145,16 @@ ck_engine::ck_engine(const std::string& spec_json) : sp(parse_spec(spec_json)) {
   reset_state();
 }
 
-ck_engine::~ck_engine() {
+ck_engine::~ck_engine() { release(); }
+
+void ck_engine::release() noexcept {
   if (stream) (void)hipStreamSynchronize(stream);
   drop_graph();
   for (auto& t : tensors)
     if (t.ptr) (void)hipFree(t.ptr);
+  tensors.clear();
+  by_name.clear();
+  plan.clear();
   if (dec_dev) (void)hipFree(dec_dev);
   if (h_warped) (void)hipHostFree(h_warped);
   if (h_packed) (void)hipHostFree(h_packed);
@@ -144,6 +162,10 @@ ck_engine::~ck_engine() {
   if (h_nv12) (void)hipHostFree(h_nv12);
   if (h_tfm) (void)hipHostFree(h_tfm);
   if (stream) (void)hipStreamDestroy(stream);
+  dec_dev = nullptr;
+  h_warped = nullptr; h_packed = nullptr; h_out = nullptr; h_nv12 = nullptr; h_tfm = nullptr;
+  stream = nullptr;
+  ws = nullptr;
 }
 
 Tensor& ck_engine::add_tensor(const std::string& name, size_t nbytes, int dtype, bool param, long rows, long cols,

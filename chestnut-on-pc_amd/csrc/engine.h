@@ -94,6 +94,8 @@ struct ck_engine {
   float time_launches(const int* idx, int n, int reps);
 
  private:
+  void init();
+  void release() noexcept;
   ck::Tensor& add_tensor(const std::string& name, size_t nbytes, int dtype, bool param, long rows = 1, long cols = 0,
                          long ld = 0);
   void build_params();

@@ -938,6 +938,13 @@ void launch_reduce(const GemmParams& p, hipStream_t s) {
   CK_LAUNCHED("splitk_reduce");
 }
 
+// A [K][N] B on the two-K-group 128x128 LDS-DMA tile is streamed into LDS as
+// it lies and read transposed (no transpose pass, no workspace for it).
+// (A and B are required to be 16-byte aligned for every launch.)
+bool bt_direct(const GemmDesc& d) {
+  return d.b_kn && d.tile == 1 && (d.K / d.split) % (2 * BK) == 0 && d.N % 128 == 0;
+}
+
 int tile_base(int tile) { const int c = tile % 10; return c > 4 ? c - 4 : c; }
 bool tile_dma(int tile) { return tile <= 9; }
 int tile_bm(int tile) { return tile == 9 ? 256 : (tile_base(tile) == 1 || tile_base(tile) == 2) ? 128 : 64; }
@@ -976,7 +983,7 @@ size_t gemm_plan(GemmDesc& d) {
   CK_REQUIRE(d.split >= 1 && d.K % (BK * d.split) == 0, "gemm: K must split into multiples of 64");
   // workspace: split-K partials, then (a [K][N] B on the LDS-DMA kernel) B transposed to [N][K] f16
   const size_t partials = (d.split > 1 || d.epi == EPI_PARTIALS) ? (size_t)d.split * d.batch * d.M * d.N : 0;
-  const size_t bt = (d.b_kn && tile_dma(d.tile)) ? ((size_t)d.batch * d.N * d.K + 1) / 2 : 0;
+  const size_t bt = (d.b_kn && tile_dma(d.tile) && !bt_direct(d)) ? ((size_t)d.batch * d.N * d.K + 1) / 2 : 0;
   return partials + bt;
 }
 
@@ -1070,8 +1077,7 @@ void launch_gemm(GemmDesc d, hipStream_t s) {
     if (d.split > 1) launch_reduce<EPI_F32>(p, s);
     return;
   }
-  if (d.b_kn && d.tile == 1 && p.kps % (2 * BK) == 0 && d.N % 128 == 0 &&
-      (reinterpret_cast<uintptr_t>(d.B) & 15) == 0) {
+  if (bt_direct(d)) {
     // the [K][N] B straight into LDS, fragments read transposed (no transpose
     // pass).  Only with two K-groups: on one (tile 5) the doubled fragment
     // reads cost more than the transpose pass saves (config 1: 44.6 against

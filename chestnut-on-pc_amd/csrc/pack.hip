@@ -28,7 +28,8 @@ __device__ __forceinline__ int wrap(long f, int n) {
 // is read from the input staging, never from the slot written in this same
 // launch, so no workgroup depends on another's store.
 //   img:    L = 5,   sample j = 0, 4        -> frames n-4 and n
-//   feat:   L = 96,  sample j = 0, 4, .., 92 -> frames n-95+4i (never n)
+//   feat:   L = 96,  sample j = 0, 4, .., 92 -> frames n-95+4i (n only when
+//           frame_skip = 1: its last sample, read from the staging)
 //   desire: L = 100, group g = max over j = 4g..4g+3 (frame n in group 24)
 // ---------------------------------------------------------------------------
 struct PolicyArgs {
@@ -68,8 +69,8 @@ __global__ __launch_bounds__(256) void policy_inputs_kernel(const PolicyArgs a) 
   const float* prev_feat = a.packed + a.desire_len + 4;
   if (i < a.n_feat) {   // feat_hist x feat_len samples
     const int k = (int)(i / a.feat_len), c = (int)(i % a.feat_len);
-    const int slot = wrap(n - (fL - 1) + (long)a.fs * k, fL);
-    a.feat_out[i] = a.feat_ring[(long)slot * a.feat_len + c];
+    const long f = n - (fL - 1) + (long)a.fs * k;
+    a.feat_out[i] = (f == n) ? prev_feat[c] : a.feat_ring[(long)wrap(f, fL) * a.feat_len + c];
     return;
   }
   i -= a.n_feat;

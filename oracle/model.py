@@ -88,6 +88,9 @@ def attention(qkv, n_heads, head_dim, acc=np.float64):
 
     S = (q k^T) / sqrt(head_dim) in f32-or-better, P = softmax(S) rounded to
     f16, O = f16(P v).  Returns f32 [T, d] (f16 values).
+    Pinned by: a brute-force loop; identical keys average the values; a
+    two-key closed form with weights 1/4, 3/4 per head that fails with Q and
+    K swapped or the scale dropped (tests/test_oracle_model_pins.py).
     """
     T = qkv.shape[0]
     d = n_heads * head_dim
@@ -103,7 +106,16 @@ def attention(qkv, n_heads, head_dim, acc=np.float64):
 
 
 def block_forward(x, weights, l, spec, acc=np.float64):
-    """One pre-LN transformer block on the f32 residual x [T, d]."""
+    """One pre-LN transformer block on the f32 residual x [T, d]:
+    x += O(attn(QKV(f16 LN1(x)))); x += down(f16 gelu(up(f16 LN2(x)))).
+
+    Pinned by (tests/test_oracle_model_pins.py, with planted mistakes in
+    tests/test_oracle_mutants.py): zero output projections return x bit for
+    bit; qkv.w = 0 gives uniform attention returning the V bias (closed form
+    through O-proj); LayerNorm gains of zero make block(x) - x one vector for
+    every input, computed in closed form (pre-LN, both residuals, biases,
+    GELU).
+    """
     eps = spec.get('ln_eps', 1e-5)
     H, hd = spec['n_heads'], spec['head_dim']
     p = f'blk.{l}.'
@@ -118,7 +130,15 @@ def block_forward(x, weights, l, spec, acc=np.float64):
 
 
 def embed(inputs, weights, spec, acc=np.float64, trace=None):
-    """Stem + temporal context + token embedding -> residual X0 [T, d] f32."""
+    """Stem + temporal context + token embedding -> residual X0 [T, d] f32:
+    X0 = tokens W_emb^T + b_emb + pos + ctx,
+    ctx = W_ctx [gelu(W_tmp feat + b_tmp) | desire | traffic | action_t] + b_ctx
+    (the context inputs in run_policy's order, compile_modeld.py:198-221).
+
+    Pinned by (tests/test_oracle_model_pins.py): emb.w = 0 gives
+    b + pos + ctx per row; one-hot ctx.w / tmp.w rows select each part of the
+    context input; one-hot emb.w rows select stem channels of each stream.
+    """
     n_stem = len(spec['stem'])
     out0 = stem_forward(inputs['img'], weights, 0, n_stem, acc)
     out1 = stem_forward(inputs['big_img'], weights, 1, n_stem, acc)
@@ -140,8 +160,14 @@ def embed(inputs, weights, spec, acc=np.float64, trace=None):
 
 
 def head_forward(x, packed, weights, spec, trace=None):
-    """Final LN + token mean-pool, GRU hidden update, linear heads.
-    Returns the output vector f32 [sum(head sizes) + hidden]."""
+    """Final LN + token mean-pool, GRU hidden update (gates r | z | n,
+    n = tanh(gi_n + r * gh_n), h = (1 - z) n + z h_prev), linear heads.
+    Returns the output vector f32 [sum(head sizes) + hidden].
+
+    Pinned by (tests/test_oracle_model_pins.py): gates saturated by +-60
+    biases (r = 1, z = 0: tanh(gi_n + gh_n); r = 0: tanh(gi_n); z = 1: h_prev
+    for either r); rows whose LayerNorm is +-v give a token mean of v / 2.
+    """
     eps = spec.get('ln_eps', 1e-5)
     Hh = spec['hidden']
     xf = layernorm(x, weights['lnf.g'], weights['lnf.b'], eps).astype(np.float32)
@@ -175,7 +201,8 @@ class OracleModel:
         self.acc = acc
         self.queues = PolicyQueues(img_h=spec.get('img_h', 128), img_w=spec.get('img_w', 256),
                                    feat_hist=spec.get('feat_hist', 24), feat_len=spec.get('feat_len', 512),
-                                   desire_hist=spec.get('desire_hist', 25), desire_len=spec.get('desire_len', 8))
+                                   desire_hist=spec.get('desire_hist', 25), desire_len=spec.get('desire_len', 8),
+                                   fs=spec.get('frame_skip', 4))
         self.trace = {}
 
     def run_frame(self, warped, packed):

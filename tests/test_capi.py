@@ -65,8 +65,13 @@ def test_gemm_planner_host_logic():
     t, s, nb = ctypes.c_int(0), ctypes.c_int(0), ctypes.c_size_t()
     # config 1: 1024 x 1024 output, K = 6144 -> 64 tiles of 128x128, split to fill 256 CUs
     _lib.call('ck_gemm_workspace', 1024, 1024, 6144, 1, ctypes.byref(t), ctypes.byref(s), ctypes.byref(nb))
-    # workspace: 4 split-K partial planes + B transposed to [N][K] f16
-    assert t.value == 1 and s.value == 4 and nb.value == 4 * 1024 * 1024 * 4 + 1024 * 6144 * 2
+    # workspace: the 4 split-K partial planes only (tile 1 reads the [K][N] B
+    # transposed out of LDS, no transposed copy)
+    assert t.value == 1 and s.value == 4 and nb.value == 4 * 1024 * 1024 * 4
+    # one K-group (tile 5) transposes B into the workspace tail first
+    t, s = ctypes.c_int(5), ctypes.c_int(4)
+    _lib.call('ck_gemm_workspace', 1024, 1024, 6144, 1, ctypes.byref(t), ctypes.byref(s), ctypes.byref(nb))
+    assert nb.value == 4 * 1024 * 1024 * 4 + 1024 * 6144 * 2
     t, s = ctypes.c_int(0), ctypes.c_int(0)
     # 1B MLP-up: 512 x 8192 -> 256 tiles, no split
     _lib.call('ck_gemm_workspace', 512, 8192, 2048, 0, ctypes.byref(t), ctypes.byref(s), ctypes.byref(nb))

@@ -44,7 +44,14 @@ def test_warp_nv12_bit_exact(gpu):
 def test_warp_nv12_rejects_short_buffer(gpu):
     from chestnut import kernels as K
     torch = gpu
+    import ctypes
+    from chestnut._lib import call
     f = torch.zeros(1000, dtype=torch.uint8, device='cuda')
     m = torch.eye(3, device='cuda')
-    with pytest.raises(RuntimeError, match='frame buffer smaller'):
+    out = torch.empty(2, 6, 128, 256, dtype=torch.uint8, device='cuda')
+    with pytest.raises(ValueError, match='must hold'):        # the torch harness, before any launch
         K.warp_nv12(f, f, m, m, **CAM)
+    p = lambda t: ctypes.c_void_p(t.data_ptr())              # noqa: E731
+    with pytest.raises(RuntimeError, match='frame buffer smaller'):   # the native entry point's own check
+        call('ck_warp_nv12', p(f), p(f), f.numel(), p(m), p(m), CAM['cam_w'], CAM['cam_h'], CAM['stride'],
+             CAM['y_height'], 512, 256, p(out), None)
