@@ -52,6 +52,8 @@ _SIGS = {
     'ck_gemm_workspace': (c_int, [c_int, c_int, c_int, c_int, P(c_int), P(c_int), P(c_size_t)]),
     'ck_gemm': (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_long, c_long, c_long,
                         c_int, c_int, c_int, c_void_p, c_size_t, c_void_p]),
+    'ck_gemm_noalloc': (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_long, c_long, c_long,
+                                c_int, c_int, c_int, c_void_p]),
     'ck_gemm_epi': (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_long, c_long, c_long,
                             c_int, c_int, c_int, c_void_p, c_size_t, c_void_p]),
     'ck_wmma_rdna4': (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_void_p]),

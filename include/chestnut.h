@@ -171,6 +171,18 @@ int ck_gemm_workspace(int M, int N, int K, int b_kn, int* tile, int* split_k, si
 int ck_gemm(const void* A, const void* B, float* C, const float* bias, int M, int N, int K, long lda, long ldb,
             long ldc, int b_kn, int tile, int split_k, void* workspace, size_t ws_bytes, void* stream);
 
+/* ck_gemm without the workspace argument, for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  It has no counterpart in the reference.
+ * The split-K partials (and a transposed [K][N] B where the tile needs one)
+ * go to a static 32 MiB device array per GPU, held until the process ends;
+ * the call allocates nothing.  A GEMM whose workspace (ck_gemm_workspace)
+ * exceeds 32 MiB is rejected with an error.  Every call on one GPU shares
+ * that GPU's array: calls that overlap on one GPU (other streams, other
+ * threads) race.  The device of `stream` must be the current device. */
+int ck_gemm_noalloc(const void* A, const void* B, float* C, const float* bias, int M, int N, int K, long lda,
+                    long ldb, long ldc, int b_kn, int tile, int split_k, void* stream);
+
 /* f16 GEMM with a fused epilogue, as the frame plan uses it.
  * epi: 1 f16(acc+bias), 2 f16(relu(acc+bias)), 3 f16(gelu(acc+bias)),
  *      4 C f32 += acc + bias.  B is [N][K]. */

@@ -1,0 +1,87 @@
+"""ck_gemm_noalloc (the allocation-free GEMM) through the C ABI: two calls in
+a row, the second smaller, each bit-identical to ck_gemm with a caller
+workspace (the same kernels and split order), plus the oracle within the GEMM
+bound; a GEMM whose workspace exceeds the static scratch is rejected before
+any launch."""
+import ctypes
+
+import numpy as np
+import pytest
+
+from chestnut import _lib
+from oracle import kernels as OK
+
+pytestmark = pytest.mark.gpu
+U = 2.0 ** -24
+
+
+def _p(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else None
+
+
+def _stream(torch):
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _ws_bytes(M, N, K, b_kn, tile, split):
+    t, s, nb = ctypes.c_int(tile), ctypes.c_int(split), ctypes.c_size_t()
+    _lib.call('ck_gemm_workspace', M, N, K, b_kn, ctypes.byref(t), ctypes.byref(s), ctypes.byref(nb))
+    return t.value, s.value, nb.value
+
+
+def _case(torch, M, N, K, b_kn, tile, split, seed, with_bias):
+    rng = np.random.default_rng(seed)
+    A = (rng.standard_normal((M, K)) / np.sqrt(K)).astype(np.float16)
+    B = (rng.standard_normal((K, N) if b_kn else (N, K)) / 2).astype(np.float16)
+    bias = rng.standard_normal(N).astype(np.float32) if with_bias else None
+    Ad, Bd = torch.from_numpy(A).cuda(), torch.from_numpy(B).cuda()
+    bd = torch.from_numpy(bias).cuda() if with_bias else None
+    ldb = N if b_kn else K
+    # the existing entry point, with a caller workspace
+    t, s, nb = _ws_bytes(M, N, K, b_kn, tile, split)
+    ws = torch.empty(max(nb // 4, 1), dtype=torch.float32, device='cuda')
+    C_ref = torch.full((M, N), float('nan'), dtype=torch.float32, device='cuda')
+    _lib.call('ck_gemm', _p(Ad), _p(Bd), _p(C_ref), _p(bd), M, N, K, K, ldb, N, b_kn, tile, split,
+              _p(ws) if nb else None, nb, _stream(torch))
+    # the allocation-free one
+    C = torch.full((M, N), float('nan'), dtype=torch.float32, device='cuda')
+    _lib.call('ck_gemm_noalloc', _p(Ad), _p(Bd), _p(C), _p(bd), M, N, K, K, ldb, N, b_kn, tile, split,
+              _stream(torch))
+    torch.cuda.synchronize()
+    got, ref = C.cpu().numpy(), C_ref.cpu().numpy()
+    return A, B, bias, got, ref, (t, s, nb)
+
+
+def test_noalloc_gemm_two_calls_match_ck_gemm(gpu):
+    torch = gpu
+    # 1: BASELINE config 1 (1024 x 6144 x 1024, [K][N] B): tile 1, split 4,
+    #    16 MiB of partials in the scratch
+    print('[noalloc] call 1: 1024x1024x6144 b_kn', flush=True)
+    A, B, _, got, ref, (t, s, nb) = _case(torch, 1024, 1024, 6144, 1, 0, 0, 1, False)
+    assert s > 1 and nb > 0, 'the first case must use the scratch'
+    np.testing.assert_array_equal(got, ref)
+    exact = OK.gemm(A, B)
+    bound = (6144 // 16 + 32) * U * (np.abs(A.astype(np.float64)) @ np.abs(B.astype(np.float64)))
+    assert np.all(np.abs(got - exact) <= bound)
+    # 2: smaller, [N][K] B, bias, split 2 -- reuses the scratch the first call left
+    print('[noalloc] call 2: 256x384x1024 nk split 2 bias', flush=True)
+    A, B, bias, got, ref, (t, s, nb) = _case(torch, 256, 384, 1024, 0, 0, 2, 2, True)
+    assert s == 2 and nb > 0
+    np.testing.assert_array_equal(got, ref)
+    exact = OK.gemm(A, B, transB=True) + bias
+    bound = (1024 // 16 + 32) * U * ((np.abs(A.astype(np.float64)) @ np.abs(B.astype(np.float64)).T) + np.abs(bias))
+    assert np.all(np.abs(got - exact) <= bound)
+
+
+def test_noalloc_gemm_rejects_workspace_above_scratch(gpu):
+    torch = gpu
+    M, N, K = 2048, 2048, 8192
+    t, s, nb = _ws_bytes(M, N, K, 0, 1, 8)
+    assert nb > (32 << 20)
+    A = torch.zeros(M, K, dtype=torch.float16, device='cuda')
+    B = torch.zeros(N, K, dtype=torch.float16, device='cuda')
+    C = torch.zeros(M, N, dtype=torch.float32, device='cuda')
+    with pytest.raises(RuntimeError, match='static scratch'):
+        _lib.call('ck_gemm_noalloc', _p(A), _p(B), _p(C), None, M, N, K, K, K, N, 0, 1, 8, _stream(torch))
+    # nothing ran: C still zero
+    assert not C.any().item()
