@@ -242,7 +242,7 @@ def test_1b_frames_vs_oracle(gpu):
     rng = np.random.default_rng(1000)
     with Engine(sp, weights=w) as eng:
         hs = None
-        for f, (warped, packed) in enumerate(frame_inputs(rng, sp, 2)):
+        for f, (warped, packed) in enumerate(frame_inputs(rng, sp, 4)):
             if hs is not None:
                 packed[12:] = hs
             out = eng.run_frame(warped, packed)
@@ -326,3 +326,21 @@ def test_frame_tuner_runs(gpu):
     M, N, K, kind, b = TU.shapes(sp)['o']
     cands = TU.candidates(M, N, K, kind, b)
     assert all(tuple(v) in cands for v in cfg.values())
+
+
+def test_failed_create_releases_device_memory(gpu):
+    """A spec whose plan is rejected after the parameters and activations of
+    the 1B model (about 2.2 GB) are allocated: ck_create fails with the
+    planner's message and frees everything, so repeated failures do not
+    consume device memory."""
+    torch = gpu
+    bad = dict(S.get_spec('big_driving_1b'), gemm_config={'blk0.qkv': [5, 3]})   # K = 2048 does not split in 3
+    torch.cuda.synchronize()
+    free0 = torch.cuda.mem_get_info()[0]
+    for _ in range(3):
+        with pytest.raises(RuntimeError, match='split into multiples of 64'):
+            Engine(bad, weights={})
+    torch.cuda.synchronize()
+    free1 = torch.cuda.mem_get_info()[0]
+    print(f'[create] free before {free0 / 2**30:.2f} GiB after {free1 / 2**30:.2f} GiB', flush=True)
+    assert free0 - free1 < (512 << 20)
