@@ -1,0 +1,153 @@
+"""BASELINE configs 1-3 as stand-alone workloads for timing and rocprofv3.
+
+    python -m chestnut.configs --config 1|2|3 [--reps N] [--out PATH]
+
+Each run first copies 256 MiB device to device (the calibration dispatch the
+FETCH_SIZE / WRITE_SIZE summaries scale by), then launches the config's
+kernels `reps` times over rotating copies of the operands, so the streamed
+bytes exceed the 256 MB Infinity Cache as in a real frame, and times them
+with HIP events on the launching stream.  It writes a JSON description (what
+each launch is, its algorithmic flops and bytes, the event timing) that
+`python -m chestnut.profiling configs` joins with the kernel trace and the
+counter passes.
+
+  1  GEMM  A f16 [1024, 6144] x B f16 [6144, 1024] -> C f32 (N(0,1)/sqrt(6144)),
+     the [K][N] B of the baseline, tile and split chosen by the planner
+  2  GEMV  W f16 [3072, 12288] ~ N(0, 0.02), x f32 ~ U(-1, 1) -> f32 [3072]
+  3  one pre-LN block of the 1B model (d 2048, 16 x 128 heads, T 512, MLP
+     8192), x ~ N(0, 1): the plan entries blkL.ln1 .. blk(L+1).ln1 of a
+     4-block engine, each block with its own 100 MB of weights
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+COPY_BYTES = 256 << 20
+
+
+def _events(torch):
+    return torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+
+def calibration_copy(torch):
+    src = torch.ones(COPY_BYTES, dtype=torch.uint8, device='cuda')
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+
+
+def config1(torch, reps):
+    from . import kernels as K
+    M, N, Kd = 1024, 1024, 6144
+    copies = 12                       # 12 x 25 MB of operands > the 256 MB Infinity Cache
+    g = torch.Generator(device='cuda').manual_seed(1)
+    A = [(torch.randn(M, Kd, device='cuda', generator=g) / np.sqrt(Kd)).half() for _ in range(copies)]
+    B = [(torch.randn(Kd, N, device='cuda', generator=g) / np.sqrt(Kd)).half() for _ in range(copies)]
+    C = torch.empty(M, N, device='cuda')
+    tile, split, nb = K.gemm_workspace(M, N, Kd, True)
+    ws = torch.empty(max(nb // 4, 1), device='cuda')
+    for a, b in zip(A, B):
+        K.gemm(a, b, out=C, workspace=ws)
+    torch.cuda.synchronize()
+    e0, e1 = _events(torch)
+    e0.record()
+    for r in range(reps):
+        K.gemm(A[r % copies], B[r % copies], out=C, workspace=ws)
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / reps
+    flops = 2.0 * M * N * Kd
+    byts = 2.0 * (M * Kd + Kd * N) + 4.0 * M * N
+    seq = ['gemm'] + (['splitk_reduce'] if split > 1 else [])
+    return {'config': 1, 'workload': 'GEMM 1024x6144 @ 6144x1024 f16 -> f32 ([K][N] B)', 'tile': tile,
+            'split_k': split, 'workspace_bytes': nb, 'copies': copies, 'unit': 'GEMM', 'sequence': seq,
+            'units_timed': reps, 'us_per_unit': us, 'flops': flops, 'bytes': byts, 'bound': 'mfma',
+            'algorithmic': {'gemm': {'flops': flops, 'bytes': byts}}}
+
+
+def config2(torch, reps):
+    from . import kernels as K
+    rows, Kd = 3072, 12288
+    copies = 5                        # 5 x 75.5 MB > the 256 MB Infinity Cache
+    g = torch.Generator(device='cuda').manual_seed(2)
+    W = [(torch.randn(rows, Kd, device='cuda', generator=g) * 0.02).half() for _ in range(copies)]
+    x = torch.rand(Kd, device='cuda', generator=g) * 2 - 1
+    y = torch.empty(rows, device='cuda')
+    for w in W:
+        K.gemv(w, x, out=y)
+    torch.cuda.synchronize()
+    e0, e1 = _events(torch)
+    e0.record()
+    for r in range(reps):
+        K.gemv(W[r % copies], x, out=y)
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / reps
+    byts = 2.0 * rows * Kd + 4.0 * Kd + 4.0 * rows
+    return {'config': 2, 'workload': 'GEMV W f16 [3072, 12288] . x f32 -> f32 [3072]', 'copies': copies,
+            'unit': 'GEMV', 'sequence': ['gemv'], 'units_timed': reps, 'us_per_unit': us,
+            'flops': 2.0 * rows * Kd, 'bytes': byts, 'bound': 'hbm',
+            'algorithmic': {'gemv': {'flops': 2.0 * rows * Kd, 'bytes': byts}}}
+
+
+def config3(torch, reps):
+    from . import spec as S
+    from .engine import Engine
+    layers = 4                        # 4 x 100 MB of block weights > the 256 MB Infinity Cache
+    sp = dict(S.get_spec('big_driving_1b'), n_layers=layers, name='block4')
+    eng = Engine(sp)
+    try:
+        rng = np.random.default_rng(42)
+        x = rng.standard_normal((512, 2048)).astype(np.float32)
+        eng.write('x', x)
+        plan = eng.plan()
+        names = [e['name'] for e in plan]
+        lo, hi = names.index('blk0.ln1'), names.index('final.ln')
+        idx = list(range(lo, hi))      # every block's ln1 .. down (its ln1 adds the previous down's partials)
+        eng.time_launches(idx, 1)
+        ms = eng.time_launches(idx, reps)
+        # one block = 7 plan entries; the first block's ln1 has no partials to add, so
+        # the per-entry figures use block 1 (its ln1 adds block 0's MLP-down partials)
+        b1 = [i for i in idx if names[i].startswith('blk1.')]
+        seq = [names[i].split('.', 1)[1] for i in b1]
+        alg = {names[i].split('.', 1)[1]: {'flops': plan[i]['flops'], 'bytes': plan[i]['bytes'],
+                                           'kernel': plan[i]['kernel']} for i in b1}
+        return {'config': 3, 'workload': 'pre-LN block d=2048, 16x128 heads, T=512, MLP 8192 (4 blocks, own weights)',
+                'blocks_per_rep': layers, 'unit': 'block', 'sequence': seq, 'units_timed': reps * layers,
+                'us_per_unit': ms * 1e3 / (reps * layers), 'flops': sum(v['flops'] for v in alg.values()),
+                'bytes': sum(v['bytes'] for v in alg.values()), 'bound': 'mfma', 'algorithmic': alg}
+    finally:
+        eng.close()
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser(prog='python -m chestnut.configs')
+    ap.add_argument('--config', type=int, required=True, choices=(1, 2, 3))
+    ap.add_argument('--reps', type=int, default=0, help='timed launches (default: 120 / 200 / 10)')
+    ap.add_argument('--out', default=None, help='write the run description as JSON')
+    a = ap.parse_args(argv)
+    import torch
+    if not torch.cuda.is_available():
+        raise SystemExit('chestnut.configs needs a GPU')
+    calibration_copy(torch)
+    t0 = time.perf_counter()
+    reps = a.reps or {1: 120, 2: 200, 3: 10}[a.config]
+    res = {1: config1, 2: config2, 3: config3}[a.config](torch, reps)
+    res['copy_bytes'] = COPY_BYTES
+    res['wall_s'] = round(time.perf_counter() - t0, 3)
+    print(json.dumps(res), flush=True)
+    if a.out:
+        os.makedirs(os.path.dirname(os.path.abspath(a.out)), exist_ok=True)
+        with open(a.out, 'w') as fh:
+            json.dump(res, fh)
+    return 0
+
+
+if __name__ == '__main__':
+    sys.exit(main())

@@ -7,6 +7,7 @@ Runs on the CPU over files a GPU run left behind:
 
     python -m chestnut.profiling frames TRACE.csv STATS.csv PLAN.json CMD > summary.md
     python -m chestnut.profiling traffic FETCH.csv WRITE.csv PMCRUN.json CMD OUT.json > summary.md
+    python -m chestnut.profiling configs RUN.json TRACE.csv FETCH.csv WRITE.csv MFMA.csv CMD OUT.json > summary.md
 
 PLAN.json is written by ``bench.py --dump-plan``; PMCRUN.json by
 ``bench.py --pmc-run FAMILY[,FAMILY...]``, which runs the first plan entry of
@@ -166,6 +167,153 @@ def traffic_md(t, cmd):
     return '\n'.join(out) + '\n'
 
 
+PEAK_TFLOPS, PEAK_GBS, N_CU, N_SIMD, N_XCD = 2500.0, 8000.0, 256, 1024, 8
+MFMA_COUNTERS = ('SQ_INSTS_VALU_MFMA_MOPS_F16', 'SQ_VALU_MFMA_BUSY_CYCLES', 'SQ_BUSY_CU_CYCLES', 'GRBM_GUI_ACTIVE')
+
+
+def _is_ck(name):
+    return 'ck::' in name or '_ZN2ck' in name
+
+
+def _units(values, run):
+    """The ck dispatches of the timed units, grouped by sequence position:
+    {entry: [value per timed unit]} from a dispatch-ordered list."""
+    seq, n = run['sequence'], run['units_timed']
+    vals = values[-n * len(seq):]
+    if len(vals) < n * len(seq):
+        raise SystemExit(f'expected {n * len(seq)} dispatches, found {len(vals)}')
+    skip = run.get('blocks_per_rep', 0)
+    out = {e: [] for e in seq}
+    for u in range(n):
+        if skip and u % skip == 0:
+            continue          # the first block of a pass: its ln1 has no partials to add
+        for k, e in enumerate(seq):
+            out[e].append(vals[u * len(seq) + k])
+    return out
+
+
+def _counter_all(path):
+    """{counter: [(dispatch, kernel, value)]} of a counter-collection CSV."""
+    out = {}
+    for r in csv.DictReader(open(path)):
+        out.setdefault(r['Counter_Name'], []).append((int(r['Dispatch_Id']), r['Kernel_Name'],
+                                                     float(r['Counter_Value'])))
+    for v in out.values():
+        v.sort()
+    return out
+
+
+def configs(run_json, trace_csv, fetch_csv=None, write_csv=None, mfma_csv=None):
+    """Per-kernel summary of a `chestnut.configs` run: trace durations, HBM
+    traffic (FETCH_SIZE / WRITE_SIZE scaled by the calibration copy), MFMA
+    counters, against the algorithmic work."""
+    run = json.load(open(run_json))
+    rows = list(csv.DictReader(open(trace_csv)))
+    rows.sort(key=lambda r: int(r['Start_Timestamp']))
+    ck = [(r['Kernel_Name'], (int(r['End_Timestamp']) - int(r['Start_Timestamp'])) / 1e3) for r in rows
+          if _is_ck(r['Kernel_Name'])]
+    durs = _units([d for _, d in ck], run)
+    names = _units([n for n, _ in ck], run)
+    res = {'run': run, 'entries': {}}
+    for e in run['sequence']:
+        d = durs[e]
+        res['entries'][e] = {'kernel': names[e][0], 'n': len(d), 'mean_us': statistics.mean(d),
+                             'median_us': statistics.median(d), 'min_us': min(d)}
+    for path, counters in ((fetch_csv, ('FETCH_SIZE',)), (write_csv, ('WRITE_SIZE',)), (mfma_csv, MFMA_COUNTERS)):
+        if not path:
+            continue
+        allc = _counter_all(path)
+        for c in counters:
+            key = next((k for k in allc if k.startswith(c)), None)
+            if key is None:
+                continue
+            seqv = allc[key]
+            ckv = [v for _, n, v in seqv if _is_ck(n)]
+            per = _units(ckv, run)
+            for e in run['sequence']:
+                res['entries'][e][c] = statistics.median(per[e])
+            if c in ('FETCH_SIZE', 'WRITE_SIZE'):
+                copy = max(v for _, n, v in seqv if 'copyBuffer' in n)
+                res[c + '_factor'] = run['copy_bytes'] / (copy * 1024.0)
+                res[c + '_copy_kib'] = copy
+    return res
+
+
+def configs_md(res, cmd):
+    run = res['run']
+    alg = run['algorithmic']
+    unit_us = sum(e['median_us'] for e in res['entries'].values())
+    t_min = max(run['flops'] / (PEAK_TFLOPS * 1e6), run['bytes'] / (PEAK_GBS * 1e3))
+    out = [f"# BASELINE config {run['config']}: {run['workload']}", '',
+           'Commands (run from the repository root on the MI355X box; the counter passes each a run of their own):',
+           '', '```', cmd, '```', '',
+           f"Timed: {run['units_timed']} {run['unit']}s over rotating operand copies (more than the 256 MB Infinity "
+           f"Cache), after one untimed pass.  Kernel trace: {unit_us:.2f} us per {run['unit']} (the sum of the "
+           f"per-kernel medians).  Algorithmic work per {run['unit']}: {run['flops'] / 1e9:.3f} GFLOP, "
+           f"{run['bytes'] / 1e6:.2f} MB; roofline floor t_min = max(flops / 2.5 PFLOP/s, bytes / 8 TB/s) = "
+           f"{t_min:.2f} us, so the {run['unit']} runs at {t_min / unit_us:.3f} of its roofline.  (The HIP-event "
+           f"time of the traced run, {run['us_per_unit']:.2f} us per {run['unit']}, includes the tracer's own "
+           'per-launch host cost.)', '']
+    if 'split_k' in run:
+        out += [f"Planner choice: tile {run['tile']}, split-K {run['split_k']}, workspace {run['workspace_bytes']} B.",
+                '']
+    out += ['| kernel | dispatches | median us | mean us | min us | algorithmic | achieved | fraction of peak |',
+            '|---|---:|---:|---:|---:|---|---|---:|']
+    for e, r in res['entries'].items():
+        a = alg.get(e)
+        if a and a['flops'] and a['flops'] / max(a['bytes'], 1) > PEAK_TFLOPS * 1e12 / (PEAK_GBS * 1e9):
+            ach = a['flops'] / (r['median_us'] * 1e-6) / 1e12
+            cols = f"{a['flops'] / 1e9:.3f} GFLOP | {ach:.1f} TFLOP/s | {ach / PEAK_TFLOPS:.3f}"
+        elif a:
+            ach = a['bytes'] / (r['median_us'] * 1e-6) / 1e9
+            cols = f"{a['bytes'] / 1e6:.2f} MB | {ach:.0f} GB/s | {ach / PEAK_GBS:.3f}"
+        else:
+            cols = '(part of the GEMM) | | '
+        name = r['kernel'].replace('(anonymous namespace)', '(anon)')
+        name = name[:70] + '...' if len(name) > 70 else name
+        out.append(f"| {e}: `{name}` | {r['n']} | {r['median_us']:.2f} | {r['mean_us']:.2f} | {r['min_us']:.2f} | "
+                   f"{cols} |")
+    if 'FETCH_SIZE_factor' in res and 'WRITE_SIZE_factor' in res:
+        ff, wf = res['FETCH_SIZE_factor'], res['WRITE_SIZE_factor']
+        out += ['', f"HBM traffic per dispatch (median), FETCH_SIZE x {ff:.4f} and WRITE_SIZE x {wf:.4f}: the "
+                f"factors make the counters of a {run['copy_bytes']} B device-to-device copy read "
+                f"{run['copy_bytes']} B and write {run['copy_bytes']} B (copy: {res['FETCH_SIZE_copy_kib']:.0f} / "
+                f"{res['WRITE_SIZE_copy_kib']:.0f} KiB).", '',
+                '| kernel | FETCH_SIZE KiB | WRITE_SIZE KiB | read B | written B | traffic B | algorithmic B | '
+                'traffic / algorithmic |', '|---|---:|---:|---:|---:|---:|---:|---:|']
+        for e, r in res['entries'].items():
+            if 'FETCH_SIZE' not in r or 'WRITE_SIZE' not in r:
+                continue
+            rb, wb = r['FETCH_SIZE'] * 1024 * ff, r['WRITE_SIZE'] * 1024 * wf
+            a = alg.get(e)
+            ab = a['bytes'] if a else 0
+            ratio = f'{(rb + wb) / ab:.2f}' if ab else ''
+            out.append(f"| {e} | {r['FETCH_SIZE']:.1f} | {r['WRITE_SIZE']:.1f} | {rb:.0f} | {wb:.0f} | {rb + wb:.0f} | "
+                       f"{ab:.0f} | {ratio} |")
+    if any('SQ_VALU_MFMA_BUSY_CYCLES' in r for r in res['entries'].values()):
+        out += ['', 'MFMA counters per dispatch (median).  MOPS_F16 x 512 is the f16 matrix work the kernel issued '
+                '(it equals the algorithmic flops).  SQ_VALU_MFMA_BUSY_CYCLES sums busy cycles over the '
+                f'{N_SIMD} SIMDs (1024 flop per busy cycle: one 32x32x16 MFMA, 32768 flop, holds its SIMD 32 '
+                f'cycles); GRBM_GUI_ACTIVE sums the {N_XCD} XCDs (a calibration copy reads about 19.7-20.6 thousand '
+                f'per us, 8 x about 2.5 GHz).  MFMA busy = MFMA_BUSY / (GUI_ACTIVE / {N_XCD} x {N_SIMD}), the share '
+                'of SIMD-cycles with the matrix core busy over the dispatch as the counters see it (that window '
+                f'includes the dispatch ramp); CU busy = SQ_BUSY_CU_CYCLES / (GUI_ACTIVE / {N_XCD} x {N_CU}), the '
+                'share of CU-cycles with a wave resident.', '',
+                '| kernel | MOPS_F16 x 512 | algorithmic flops | MFMA_BUSY_CYCLES | BUSY_CU_CYCLES | GUI_ACTIVE | '
+                'MFMA busy | CU busy |', '|---|---:|---:|---:|---:|---:|---:|---:|']
+        for e, r in res['entries'].items():
+            if 'SQ_VALU_MFMA_BUSY_CYCLES' not in r:
+                continue
+            mops = r.get('SQ_INSTS_VALU_MFMA_MOPS_F16', 0) * 512
+            gui = r.get('GRBM_GUI_ACTIVE', 0)
+            busy = r['SQ_VALU_MFMA_BUSY_CYCLES'] / (gui / N_XCD * N_SIMD) if gui else 0
+            cub = r.get('SQ_BUSY_CU_CYCLES', 0) / (gui / N_XCD * N_CU) if gui else 0
+            a = alg.get(e)
+            out.append(f"| {e} | {mops:.4g} | {(a['flops'] if a else 0):.4g} | {r['SQ_VALU_MFMA_BUSY_CYCLES']:.4g} | "
+                       f"{r.get('SQ_BUSY_CU_CYCLES', 0):.4g} | {gui:.4g} | {busy:.3f} | {cub:.3f} |")
+    return '\n'.join(out) + '\n'
+
+
 def main(argv):
     if argv[0] == 'frames':
         sys.stdout.write(frames_md(argv[1], argv[2], argv[3], argv[4]))
@@ -174,6 +322,13 @@ def main(argv):
         with open(argv[5], 'w') as fh:
             json.dump(t, fh, indent=1)
         sys.stdout.write(traffic_md(t, argv[4]))
+    elif argv[0] == 'configs':
+        # configs RUN.json TRACE.csv FETCH.csv WRITE.csv MFMA.csv CMD OUT.json  ('-' for a missing pass)
+        opt = [None if x == '-' else x for x in argv[3:6]]
+        res = configs(argv[1], argv[2], *opt)
+        with open(argv[7], 'w') as fh:
+            json.dump(res, fh, indent=1)
+        sys.stdout.write(configs_md(res, argv[6]))
     else:
         raise SystemExit(__doc__)
 
