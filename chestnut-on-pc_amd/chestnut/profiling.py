@@ -203,7 +203,7 @@ def _counter_all(path):
     return out
 
 
-def configs(run_json, trace_csv, fetch_csv=None, write_csv=None, mfma_csv=None):
+def configs(run_json, trace_csv, fetch_csv=None, write_csv=None, mfma_csv=None, extra_csvs=()):
     """Per-kernel summary of a `chestnut.configs` run: trace durations, HBM
     traffic (FETCH_SIZE / WRITE_SIZE scaled by the calibration copy), MFMA
     counters, against the algorithmic work."""
@@ -219,7 +219,13 @@ def configs(run_json, trace_csv, fetch_csv=None, write_csv=None, mfma_csv=None):
         d = durs[e]
         res['entries'][e] = {'kernel': names[e][0], 'n': len(d), 'mean_us': statistics.mean(d),
                              'median_us': statistics.median(d), 'min_us': min(d)}
-    for path, counters in ((fetch_csv, ('FETCH_SIZE',)), (write_csv, ('WRITE_SIZE',)), (mfma_csv, MFMA_COUNTERS)):
+    passes = [(fetch_csv, ('FETCH_SIZE',)), (write_csv, ('WRITE_SIZE',)), (mfma_csv, MFMA_COUNTERS)]
+    res['extra'] = []
+    for path in extra_csvs:
+        names_in = sorted(_counter_all(path))
+        passes.append((path, tuple(names_in)))
+        res['extra'] += names_in
+    for path, counters in passes:
         if not path:
             continue
         allc = _counter_all(path)
@@ -311,6 +317,12 @@ def configs_md(res, cmd):
             a = alg.get(e)
             out.append(f"| {e} | {mops:.4g} | {(a['flops'] if a else 0):.4g} | {r['SQ_VALU_MFMA_BUSY_CYCLES']:.4g} | "
                        f"{r.get('SQ_BUSY_CU_CYCLES', 0):.4g} | {gui:.4g} | {busy:.3f} | {cub:.3f} |")
+    if res.get('extra'):
+        cols = res['extra']
+        out += ['', 'Further counters per dispatch (median; `_sum` counters add all instances of the block).', '',
+                '| kernel | ' + ' | '.join(cols) + ' |', '|---|' + '---:|' * len(cols)]
+        for e, r in res['entries'].items():
+            out.append(f'| {e} | ' + ' | '.join(f'{r.get(c, 0):.4g}' for c in cols) + ' |')
     return '\n'.join(out) + '\n'
 
 
@@ -323,9 +335,10 @@ def main(argv):
             json.dump(t, fh, indent=1)
         sys.stdout.write(traffic_md(t, argv[4]))
     elif argv[0] == 'configs':
-        # configs RUN.json TRACE.csv FETCH.csv WRITE.csv MFMA.csv CMD OUT.json  ('-' for a missing pass)
+        # configs RUN.json TRACE.csv FETCH.csv WRITE.csv MFMA.csv CMD OUT.json [EXTRA.csv ...]
+        # ('-' for a missing pass)
         opt = [None if x == '-' else x for x in argv[3:6]]
-        res = configs(argv[1], argv[2], *opt)
+        res = configs(argv[1], argv[2], *opt, extra_csvs=argv[8:])
         with open(argv[7], 'w') as fh:
             json.dump(res, fh, indent=1)
         sys.stdout.write(configs_md(res, argv[6]))

@@ -79,6 +79,7 @@ Spec parse_spec(const std::string& json) {
                    s.cam_y_height >= s.cam_h,
                "spec: camera needs an even width and height, stride >= width, y_height >= height");
   }
+  s.overlap = jint(o, "overlap_context", -1);
   if (const JVal* gc = o.get("gemm_config")) {
     CK_REQUIRE(gc->kind == JVal::OBJ, "spec: gemm_config must be an object {entry: [tile, split]}");
     for (const auto& kv : gc->obj) {
@@ -128,6 +129,9 @@ void ck_engine::init() {
   CK_REQUIRE(T % 64 == 0 && T <= 512, "spec: token count (last stem width) must be a multiple of 64, <= 512");
   CK_REQUIRE(2 * n_spatial % 64 == 0, "spec: token features must be a multiple of 64");
   CK_HIP(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking));
+  CK_HIP(hipStreamCreateWithFlags(&side, hipStreamNonBlocking));
+  CK_HIP(hipEventCreateWithFlags(&ev_fork, hipEventDisableTiming));
+  CK_HIP(hipEventCreateWithFlags(&ev_join, hipEventDisableTiming));
   build_params();
   build_activations();
   build_decode();
@@ -149,6 +153,7 @@ ck_engine::~ck_engine() { release(); }
 
 void ck_engine::release() noexcept {
   if (stream) (void)hipStreamSynchronize(stream);
+  if (side) (void)hipStreamSynchronize(side);
   drop_graph();
   for (auto& t : tensors)
     if (t.ptr) (void)hipFree(t.ptr);
@@ -162,6 +167,11 @@ void ck_engine::release() noexcept {
   if (h_nv12) (void)hipHostFree(h_nv12);
   if (h_tfm) (void)hipHostFree(h_tfm);
   if (stream) (void)hipStreamDestroy(stream);
+  if (side) (void)hipStreamDestroy(side);
+  if (ev_fork) (void)hipEventDestroy(ev_fork);
+  if (ev_join) (void)hipEventDestroy(ev_join);
+  side = nullptr;
+  ev_fork = ev_join = nullptr;
   dec_dev = nullptr;
   h_warped = nullptr; h_packed = nullptr; h_out = nullptr; h_nv12 = nullptr; h_tfm = nullptr;
   stream = nullptr;
@@ -435,6 +445,30 @@ void ck_engine::build_plan() {
       launch_policy_inputs(q, warped, packed, counter, ring, fr, dr, img, fb, tail, s);
     });
   }
+  // The temporal and context GEMVs depend only on the feature queue: with
+  // `overlap` they run on a second stream forked after the inputs, beside
+  // the conv stem, and the embedding waits for them.
+  const bool overlap = sp.overlap >= 0 ? sp.overlap != 0 : false;
+  auto add_context = [&](int branch) {
+    const int Kt = sp.feat_hist * sp.feat_len, Td = sp.temporal_dim;
+    const half_t* tw = h16("tmp.w");
+    const float* tb = f32("tmp.b");
+    const float* fbuf = f32("feat_buf");
+    float* cin = f32("ctx_in");
+    add("temporal", "gemv", 2.0 * Td * Kt, (double)Td * Kt * 2 + Kt * 4 + Td * 8, [=](hipStream_t s) {
+      launch_gemv(tw, fbuf, tb, cin, Td, Kt, Kt, GEMV_GELU, 0, s);
+    });
+    plan.back().branch = branch;
+    const half_t* cw = h16("ctx.w");
+    const float* cb = f32("ctx.b");
+    float* ctx = f32("ctx");
+    const int ldc = ld_ctx;
+    add("context", "gemv", 2.0 * d * ldc, (double)d * ldc * 2 + ldc * 4 + d * 8, [=](hipStream_t s) {
+      launch_gemv(cw, cin, cb, ctx, d, ldc, ldc, GEMV_NONE, 0, s);
+    });
+    plan.back().branch = branch;
+  };
+  if (overlap) add_context(1);
   bool tokens_fused = false;
   // 2. conv stem, both streams batched.  Layer 0 (u8 image, 12 channels):
   // im2col with zero-border image reads + MFMA GEMM.  Later layers (f16,
@@ -512,21 +546,8 @@ void ck_engine::build_plan() {
     const int ns = n_spatial, C5 = T;
     if (!tokens_fused)
       add("tokens", "tokens", 0, 2.0 * 2 * ns * C5 * 2, [=](hipStream_t s) { launch_tokens(so, ns, C5, tok, s); });
-    const int Kt = sp.feat_hist * sp.feat_len, Td = sp.temporal_dim;
-    const half_t* tw = h16("tmp.w");
-    const float* tb = f32("tmp.b");
-    const float* fbuf = f32("feat_buf");
-    float* cin = f32("ctx_in");
-    add("temporal", "gemv", 2.0 * Td * Kt, (double)Td * Kt * 2 + Kt * 4 + Td * 8, [=](hipStream_t s) {
-      launch_gemv(tw, fbuf, tb, cin, Td, Kt, Kt, GEMV_GELU, 0, s);
-    });
-    const half_t* cw = h16("ctx.w");
-    const float* cb = f32("ctx.b");
+    if (!overlap) add_context(0);
     float* ctx = f32("ctx");
-    const int ldc = ld_ctx;
-    add("context", "gemv", 2.0 * d * ldc, (double)d * ldc * 2 + ldc * 4 + d * 8, [=](hipStream_t s) {
-      launch_gemv(cw, cin, cb, ctx, d, ldc, ldc, GEMV_NONE, 0, s);
-    });
     const half_t* pos = h16("pos");
     const float* eb = f32("emb.b");
     float* x = f32("x");
@@ -538,6 +559,7 @@ void ck_engine::build_plan() {
     g.M = T; g.N = d; g.K = 2 * ns; g.epi = EPI_EMBED;
     g.tile = 4;   // 64x64: a one- or two-step GEMM whose time is its epilogue, spread over 4x the workgroups
     add_gemm("embed", "gemm_embed", g);
+    plan.back().join = overlap;
   }
   // 4. transformer blocks.  The two residual GEMMs (attention output, MLP
   // down) split K and leave f32 partials in the workspace; the LayerNorm that
@@ -678,11 +700,42 @@ void ck_engine::drop_graph() {
   graph_nodes = 0;
 }
 
+// The plan in order on the engine stream; entries marked `branch` go to the
+// side stream, forked from the engine stream at the first of them, and the
+// engine stream waits for the side stream at the next entry marked `join`
+// (or at the end).  The same calls serve eager frames and graph capture,
+// where the fork and join become graph edges.
+void ck_engine::launch_plan() {
+  bool forked = false, pending = false;
+  for (auto& l : plan) {
+    if (l.branch) {
+      if (!forked) {
+        CK_HIP(hipEventRecord(ev_fork, stream));
+        CK_HIP(hipStreamWaitEvent(side, ev_fork, 0));
+        forked = true;
+      }
+      l.fn(side);
+      pending = true;
+      continue;
+    }
+    if (pending && l.join) {
+      CK_HIP(hipEventRecord(ev_join, side));
+      CK_HIP(hipStreamWaitEvent(stream, ev_join, 0));
+      pending = false;
+    }
+    l.fn(stream);
+  }
+  if (pending) {
+    CK_HIP(hipEventRecord(ev_join, side));
+    CK_HIP(hipStreamWaitEvent(stream, ev_join, 0));
+  }
+}
+
 void ck_engine::capture() {
   drop_graph();
   CK_HIP(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal));
   try {
-    for (auto& l : plan) l.fn(stream);
+    launch_plan();
   } catch (...) {
     hipGraph_t g = nullptr;
     (void)hipStreamEndCapture(stream, &g);
@@ -699,7 +752,7 @@ void ck_engine::frame_launch() {
     if (!gexec) capture();
     CK_HIP(hipGraphLaunch(gexec, stream));
   } else {
-    for (auto& l : plan) l.fn(stream);
+    launch_plan();
   }
 }
 

@@ -24,6 +24,9 @@ struct Spec {
   std::vector<std::pair<std::string, int>> outputs;
   // optional NV12 camera geometry (run_frame_nv12); width 0 = none
   int cam_w = 0, cam_h = 0, cam_stride = 0, cam_y_height = 0;
+  // run the temporal and context GEMVs on a second stream beside the conv
+  // stem (-1: the engine decides by model size, 0: off, 1: on)
+  int overlap = -1;
   // optional per-plan-entry GEMM configuration {entry: [tile, split]} (A/B probes)
   std::vector<std::pair<std::string, std::pair<int, int>>> gemm_cfg;
 };
@@ -44,6 +47,8 @@ struct Launch {
   std::string name;      // plan position, e.g. "blk3.qkv"
   std::string kernel;    // kernel family, e.g. "gemm_qkv"
   double flops = 0, bytes = 0;   // algorithmic work of one launch
+  int branch = 0;        // 1: launched on the side stream (forked after the entries before it)
+  bool join = false;     // the main stream waits for the side stream before this entry
   std::function<void(hipStream_t)> fn;
 };
 
@@ -52,6 +57,8 @@ struct Launch {
 struct ck_engine {
   ck::Spec sp;
   hipStream_t stream = nullptr;
+  hipStream_t side = nullptr;                // second stream of a forked plan
+  hipEvent_t ev_fork = nullptr, ev_join = nullptr;
   std::vector<ck::Tensor> tensors;
   std::map<std::string, size_t> by_name;
   std::vector<ck::Launch> plan;
@@ -86,6 +93,7 @@ struct ck_engine {
   void run_frame_nv12(const uint8_t* frame, const uint8_t* big_frame, const float* tfm, const float* big_tfm,
                       const float* packed, float* out);
   void frame_launch();
+  void launch_plan();
   void capture();
   void drop_graph();
   void reset_state();

@@ -344,3 +344,30 @@ def test_failed_create_releases_device_memory(gpu):
     free1 = torch.cuda.mem_get_info()[0]
     print(f'[create] free before {free0 / 2**30:.2f} GiB after {free1 / 2**30:.2f} GiB', flush=True)
     assert free0 - free1 < (512 << 20)
+
+
+@pytest.mark.parametrize('graph', [True, False], ids=['graph', 'eager'])
+def test_overlapped_context_branch_is_bit_identical(tiny, graph):
+    """The temporal and context GEMVs on a side stream beside the stem (the
+    plan forked after the inputs and joined before the embedding) give the
+    same bits as the single-stream plan, frame after frame."""
+    sp, w, eng = tiny
+    rng = np.random.default_rng(15)
+    frames = list(frame_inputs(rng, sp, 4))
+    outs = []
+    for ov in (0, 1):
+        with Engine(dict(sp, overlap_context=ov), weights=w, graph=graph) as e:
+            names = [p['name'] for p in e.plan()]
+            if ov:
+                assert names.index('temporal') < names.index('stem0.conv')
+            res, hs = [], None
+            for warped, packed in frames:
+                packed = packed.copy()
+                if hs is not None:
+                    packed[12:] = hs
+                o = e.run_frame(warped, packed)
+                hs = o[e.out_slices['hidden_state']]
+                res.append(o)
+            outs.append(res)
+    for a, b in zip(*outs):
+        np.testing.assert_array_equal(a, b)
