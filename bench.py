@@ -89,7 +89,8 @@ def micro(torch):
     us = e0.elapsed_time(e1) * 1e3 / (reps * n_copies)
     by = 3072 * 12288 * 2 + 12288 * 4 + 3072 * 4
     res['gemv_config2'] = {'shape': [3072, 12288], 'us': round(us, 2), 'gbs': round(by / us / 1e3, 1),
-                           'frac_hbm': round(by / us / 1e3 / PEAK_HBM_GBS, 4), 'copies': n_copies}
+                           'frac_hbm': round(by / us / 1e3 / PEAK_HBM_GBS, 4), 'copies': n_copies,
+                           'profile': profile_record('gemv_config2_3072x12288')}
     del W
     n_copies = 12
     A = [torch.randn(1024, 6144, device='cuda', dtype=torch.float16) / 78.4 for _ in range(n_copies)]
@@ -111,7 +112,7 @@ def micro(torch):
     fl = 2.0 * 1024 * 1024 * 6144
     res['gemm_config1'] = {'shape': [1024, 6144, 1024], 'us': round(us, 2), 'tflops': round(fl / us / 1e6, 1),
                            'frac_mfma': round(fl / us / 1e6 / PEAK_F16_TFLOPS, 4), 'tile': tile, 'split_k': split,
-                           'copies': n_copies}
+                           'copies': n_copies, 'profile': profile_record('gemm_config1_1024x6144x1024')}
     # NV12 road-camera warp of both frames (the step before `warped`)
     cam = S.ROAD_CAMERA
     nb = S.nv12_bytes(cam)
@@ -138,6 +139,45 @@ def micro(torch):
     res['warp_nv12'] = {'camera': [cam['width'], cam['height']], 'model': [512, 256], 'us': round(us, 2),
                         'out_bytes': wout.numel()}
     return res
+
+
+def profile_record(name):
+    """Per-kernel figures of a committed BASELINE-config profile
+    (profiles/NAME.json, written by `python -m chestnut.profiling configs`):
+    kernel-trace median us, HBM traffic per dispatch (copy-calibrated
+    FETCH_SIZE + WRITE_SIZE) and MFMA busy, with the summary's path."""
+    path = os.path.join(ROOT, 'profiles', name + '.json')
+    try:
+        with open(path) as fh:
+            r = json.load(fh)
+    except (OSError, ValueError):
+        return None
+    ff, wf = r.get('FETCH_SIZE_factor'), r.get('WRITE_SIZE_factor')
+    out = {'source': os.path.relpath(path[:-5] + '.md', ROOT), 'kernels': {}}
+    for e, v in r['entries'].items():
+        k = {'trace_median_us': round(v['median_us'], 2)}
+        if ff and 'FETCH_SIZE' in v and 'WRITE_SIZE' in v:
+            k['traffic_bytes'] = round(v['FETCH_SIZE'] * 1024 * ff + v['WRITE_SIZE'] * 1024 * wf)
+        if v.get('GRBM_GUI_ACTIVE') and 'SQ_VALU_MFMA_BUSY_CYCLES' in v:
+            k['mfma_busy'] = round(v['SQ_VALU_MFMA_BUSY_CYCLES'] / (v['GRBM_GUI_ACTIVE'] / 8 * 1024), 3)
+        out['kernels'][e] = k
+    out['trace_us_per_unit'] = round(sum(v['median_us'] for v in r['entries'].values()), 2)
+    return out
+
+
+def config3_from_table(rows):
+    """BASELINE config 3 (one d=2048 pre-LN block) live: the in-frame family
+    timings of one block's seven kernels, against the block's 53.7 GFLOP."""
+    fams = ('blk.ln1', 'blk.qkv', 'blk.attn', 'blk.o', 'blk.ln2', 'blk.up', 'blk.down')
+    by = {r['name']: r for r in rows}
+    if not all(f in by for f in fams):
+        return None
+    us = sum(by[f]['us_avg'] for f in fams)
+    fl = sum(by[f]['flops'] for f in fams)
+    t_min = fl / (PEAK_F16_TFLOPS * 1e6)
+    return {'workload': 'one pre-LN block d=2048, 16x128 heads, T=512, MLP 8192 (in-frame family timing)',
+            'us_per_block': round(us, 2), 'gflop': round(fl / 1e9, 3), 'tflops': round(fl / us / 1e6, 1),
+            'frac_roofline': round(t_min / us, 4), 'profile': profile_record('block_config3_d2048_t512')}
 
 
 def config4_fps(frames=200):
@@ -365,6 +405,9 @@ def main():
                        'host_inclusive_fps': round(host_fps, 2),
                        'nv12_host_inclusive_fps': round(nv12_fps, 2)},
             'roofline': roof, 'kernels': rows}
+    c3 = config3_from_table(rows)
+    if c3:
+        line['config3'] = c3
     if not a.no_micro:
         line['micro'] = micro(torch)
         log(f'[bench] micro {line["micro"]}')
