@@ -280,6 +280,7 @@ int ck_write_tensor(ck_engine* e, const char* name, const void* host, size_t nby
   if (t.param) {
     e->upload(name, host, nbytes);
   } else {
+    CK_REQUIRE(t.ld == t.cols, std::string("ck_write_tensor: padded tensor ") + name);
     CK_HIP(hipStreamSynchronize(e->stream));
     CK_HIP(hipMemcpy(t.ptr, host, nbytes, hipMemcpyHostToDevice));
   }

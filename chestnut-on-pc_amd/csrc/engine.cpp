@@ -14,6 +14,7 @@
 // advanced by the plan's own kernels.
 #include "engine.h"
 
+#include <cmath>
 #include <cstring>
 #include <sstream>
 
@@ -25,14 +26,21 @@ namespace {
 
 long round_up(long v, long m) { return (v + m - 1) / m * m; }
 
+// An integral JSON number within int range (what = the key, for the message).
+int as_int(const JVal& v, const std::string& what) {
+  CK_REQUIRE(v.kind == JVal::NUM, "spec: " + what + " must be a number");
+  CK_REQUIRE(std::isfinite(v.num) && v.num == std::floor(v.num) && std::fabs(v.num) < 2147483648.0,
+             "spec: " + what + " must be an integer");
+  return (int)v.num;
+}
+
 int jint(const JVal& o, const char* k, int dflt, bool required = false) {
   const JVal* v = o.get(k);
   if (!v) {
     CK_REQUIRE(!required, std::string("spec: missing key ") + k);
     return dflt;
   }
-  CK_REQUIRE(v->kind == JVal::NUM, std::string("spec: key ") + k + " must be a number");
-  return (int)v->num;
+  return as_int(*v, std::string("key ") + k);
 }
 
 }  // namespace
@@ -58,15 +66,21 @@ Spec parse_spec(const std::string& json) {
   s.n_layers = jint(o, "n_layers", 0, true);
   s.d_ff = jint(o, "d_ff", 0, true);
   s.temporal_dim = jint(o, "temporal_dim", 0, true);
-  if (const JVal* v = o.get("ln_eps")) s.eps = (float)v->num;
+  if (const JVal* v = o.get("ln_eps")) {
+    CK_REQUIRE(v->kind == JVal::NUM && v->num > 0 && std::isfinite(v->num), "spec: ln_eps must be a positive number");
+    s.eps = (float)v->num;
+  }
   const JVal* st = o.get("stem");
   CK_REQUIRE(st && st->kind == JVal::ARR && !st->arr.empty(), "spec: stem must be a non-empty array");
-  for (const auto& e : st->arr) s.stem.push_back((int)e.num);
+  for (const auto& e : st->arr) s.stem.push_back(as_int(e, "stem width"));
   if (const JVal* ou = o.get("outputs")) {
     CK_REQUIRE(ou->kind == JVal::ARR, "spec: outputs must be an array of [name, size]");
     for (const auto& e : ou->arr) {
-      CK_REQUIRE(e.kind == JVal::ARR && e.arr.size() == 2, "spec: outputs entries are [name, size]");
-      s.outputs.emplace_back(e.arr[0].str, (int)e.arr[1].num);
+      CK_REQUIRE(e.kind == JVal::ARR && e.arr.size() == 2 && e.arr[0].kind == JVal::STR,
+                 "spec: outputs entries are [name, size]");
+      const int n = as_int(e.arr[1], "output size");
+      CK_REQUIRE(n > 0, "spec: output sizes must be positive");
+      s.outputs.emplace_back(e.arr[0].str, n);
     }
   }
   if (const JVal* cam = o.get("camera")) {
@@ -85,10 +99,17 @@ Spec parse_spec(const std::string& json) {
     for (const auto& kv : gc->obj) {
       CK_REQUIRE(kv.second.kind == JVal::ARR && kv.second.arr.size() == 2,
                  "spec: gemm_config entries are [tile, split]");
-      s.gemm_cfg.push_back({kv.first, {(int)kv.second.arr[0].num, (int)kv.second.arr[1].num}});
+      s.gemm_cfg.push_back({kv.first, {as_int(kv.second.arr[0], "gemm_config tile"),
+                                       as_int(kv.second.arr[1], "gemm_config split")}});
     }
   }
   // structural requirements of the kernels
+  CK_REQUIRE(s.img_h > 0 && s.img_w > 0 && s.feat_len > 0 && s.feat_hist > 0 && s.desire_len > 0 &&
+                 s.desire_hist > 0 && s.d > 0 && s.n_heads > 0 && s.n_layers > 0 && s.d_ff > 0 && s.temporal_dim > 0,
+             "spec: sizes, counts and widths must be positive");
+  for (int c : s.stem) CK_REQUIRE(c > 0, "spec: stem widths must be positive");
+  CK_REQUIRE(s.head_dim == 64 || s.head_dim == 128, "spec: head_dim must be 64 or 128");
+  CK_REQUIRE(s.feat_len % 8 == 0, "spec: feat_len must be a multiple of 8");
   CK_REQUIRE(s.n_frames == 2, "spec: n_frames must be 2 (two sampled frames per stream)");
   CK_REQUIRE(s.fs >= 1, "spec: frame_skip must be >= 1");
   CK_REQUIRE(s.d == s.n_heads * s.head_dim, "spec: d_model must equal n_heads * head_dim");

@@ -40,6 +40,29 @@ def test_bad_spec_raises_with_message():
         _lib.call('ck_create', S.spec_json(odd).encode(), ctypes.byref(ctypes.c_void_p()))
 
 
+@pytest.mark.parametrize('change,message', [
+    (dict(stem=[8, 16, 'x', 64, 64]), 'stem width must be a number'),
+    (dict(stem=[8, 16, 32, 64, 0]), 'stem widths must be positive'),
+    (dict(n_layers=0), 'must be positive'),
+    (dict(img_h=0), 'must be positive'),
+    (dict(feat_hist=-3), 'must be positive'),
+    (dict(d_model=256, n_heads=8, head_dim=32), 'head_dim must be 64 or 128'),
+    (dict(feat_len=20, hidden=20), 'feat_len must be a multiple of 8'),
+    (dict(d_ff=512.5), 'd_ff must be an integer'),
+    (dict(frame_skip=1e12), 'frame_skip must be an integer'),
+    (dict(ln_eps=0), 'ln_eps must be a positive number'),
+    (dict(outputs=[['plan', 0]]), 'output sizes must be positive'),
+    (dict(outputs=[[3, 10]]), 'outputs entries are'),
+    (dict(gemm_config={'blk0.up': ['a', 1]}), 'gemm_config tile must be a number'),
+])
+def test_spec_fields_are_checked_before_any_allocation(change, message):
+    # parse_spec runs before the engine touches the GPU, so a bad field is
+    # reported by name here, not as a HIP failure
+    bad = dict(S.get_spec('tiny'), **change)
+    with pytest.raises(RuntimeError, match=message):
+        _lib.call('ck_create', S.spec_json(bad).encode(), ctypes.byref(ctypes.c_void_p()))
+
+
 def test_nv12_bytes():
     # Y plane 2048 x 1216 plus 604 UV rows of 2048 bytes
     assert S.nv12_bytes(S.ROAD_CAMERA) == 2048 * 1216 + 604 * 2048
