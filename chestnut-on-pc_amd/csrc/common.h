@@ -36,6 +36,31 @@ typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
 typedef float float16_t __attribute__((ext_vector_type(16)));
+typedef unsigned u32x2_t __attribute__((ext_vector_type(2)));
+typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
+
+// Stores with the device-scope cache policy (sc1), for data that the next
+// kernel of the frame reads.  On the 1B and 39M frames they beat both the
+// default and the non-temporal policy.  No global-store builtin takes the
+// policy bits, so they go through a raw buffer resource (base = a
+// wave-uniform pointer, byte offsets per lane), which the compiler schedules
+// and tracks like any other store.  Callers keep a region below 2^31 bytes
+// (sc1_ok) and otherwise store as before.
+constexpr int CPOL_SC1 = 16;             // cache-policy operand: sc1
+constexpr int BUF_WORD3 = 0x00020000;    // raw 32-bit buffer, no swizzle
+__device__ __forceinline__ bool sc1_ok(long bytes) { return bytes > 0 && bytes < (1L << 31); }
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t sc1_rsrc(const void* base, long bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, BUF_WORD3);
+}
+__device__ __forceinline__ void store_sc1(__amdgpu_buffer_rsrc_t r, long off, float4_t v) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, v), r, (int)off, 0, CPOL_SC1);
+}
+__device__ __forceinline__ void store_sc1(__amdgpu_buffer_rsrc_t r, long off, half8_t v) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, v), r, (int)off, 0, CPOL_SC1);
+}
+__device__ __forceinline__ void store_sc1(__amdgpu_buffer_rsrc_t r, long off, half4_t v) {
+  __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2_t, v), r, (int)off, 0, CPOL_SC1);
+}
 
 // ---------------------------------------------------------------------------
 // Wave64 reductions.  Lanes 0..63 of a CDNA wave form 4 DPP rows of 16.

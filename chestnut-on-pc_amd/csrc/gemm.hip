@@ -349,10 +349,11 @@ __device__ __forceinline__ void dma_issue(const half_t* const* asrc, const half_
 // columns are staged transposed ([n][m]), four consecutive rows of a lane
 // forming one 8-byte LDS write, so V^T rows leave contiguously as well.
 // Row pitches carry 16 bytes of padding so the two half-waves' staging
-// writes (rows r and r+4) fall in different banks.  The row-major outputs
-// and the split-K partials leave with non-temporal stores: written once and
-// read by the next kernel, they gain nothing from allocating in this XCD's
-// L2 (measured: 0.9% of the 1B frame).
+// writes (rows r and r+4) fall in different banks.  The split-K partials and
+// the row-major f16 outputs, read by the next kernel, leave with the
+// device-scope cache policy (store_sc1: -0.5% and -0.4% of the 1B frame
+// against non-temporal stores, which were themselves 0.9% ahead of default
+// stores); the f32 outputs with non-temporal stores.
 // Requires (checked on the host, else the direct per-element stores run):
 // N % 8 == 0, ldc / batch stride / base of C and ws 16-byte compatible,
 // and for QKV qk_cols % BN == 0, M % 8 == 0 and vt_ld % 8 == 0.
@@ -392,6 +393,9 @@ __device__ __forceinline__ void store_staged(const GemmParams& p, const float16_
     constexpr int CPR = WN / 4;   // 16-byte chunks per row
     float* dst = to_ws ? p.ws + ((long)sp * p.batch + bz) * (long)p.M * p.N : static_cast<float*>(p.C) + bz * p.sC;
     const long ld = to_ws ? p.N : p.ldc;
+    const long plane = to_ws ? 4L * p.M * p.N : 0;   // the partials' plane, stored with sc1
+    const bool sc1 = to_ws && sc1_ok(plane);
+    const __amdgpu_buffer_rsrc_t rs = sc1_rsrc(dst, sc1 ? plane : 0);
 #pragma unroll 4
     for (int q = lane; q < WM * CPR; q += 64) {
       const int r = q / CPR, c = (q % CPR) * 4;
@@ -405,7 +409,8 @@ __device__ __forceinline__ void store_staged(const GemmParams& p, const float16_
         const float4_t cs = *reinterpret_cast<const float4_t*>(p.ctx + n);
         v += float4_t{(float)ps[0] + cs[0], (float)ps[1] + cs[1], (float)ps[2] + cs[2], (float)ps[3] + cs[3]};
       }
-      __builtin_nontemporal_store(v, g);
+      if (sc1) store_sc1(rs, ((long)m * ld + n) * 4, v);
+      else __builtin_nontemporal_store(v, g);
     }
     return;
   }
@@ -501,13 +506,17 @@ __device__ __forceinline__ void store_staged(const GemmParams& p, const float16_
   }
   constexpr int CPR = WN / 8;
   half_t* dst = static_cast<half_t*>(p.C) + bz * p.sC;
+  const long span = 2L * ((long)(p.M - 1) * p.ldc + p.N);   // bytes of this batch's output
+  const bool sc1 = sc1_ok(span);
+  const __amdgpu_buffer_rsrc_t rs = sc1_rsrc(dst, sc1 ? span : 0);
 #pragma unroll 4
   for (int q = lane; q < WM * CPR; q += 64) {
     const int r = q / CPR, c = (q % CPR) * 8;
     const int m = mw + r, n = nw + c;
     if (m >= p.M || n >= p.N) continue;
-    __builtin_nontemporal_store(*reinterpret_cast<const half8_t*>(st + r * PH + c),
-                                reinterpret_cast<half8_t*>(dst + (long)m * p.ldc + n));
+    const half8_t v = *reinterpret_cast<const half8_t*>(st + r * PH + c);
+    if (sc1) store_sc1(rs, ((long)m * p.ldc + n) * 2, v);
+    else __builtin_nontemporal_store(v, reinterpret_cast<half8_t*>(dst + (long)m * p.ldc + n));
   }
 }
 
