@@ -183,8 +183,9 @@ __global__ __launch_bounds__(64 * att_waves(NKT)) void attention_kernel(const ha
       acc += f * *reinterpret_cast<const float4_t*>(&part[w][q][c]);
     }
     const float rden = 1.0f / den;
-    *reinterpret_cast<half4_t*>(out + (long)(q0 + q) * d + h * HD + c) =
-        half4_t{(half_t)(acc[0] * rden), (half_t)(acc[1] * rden), (half_t)(acc[2] * rden), (half_t)(acc[3] * rden)};
+    // device-scope cache policy for the output the O-projection reads next (-0.4% of the 1B frame)
+    store_sc1(sc1_rsrc(out, 2L * T * d), ((long)(q0 + q) * d + h * HD + c) * 2,
+              half4_t{(half_t)(acc[0] * rden), (half_t)(acc[1] * rden), (half_t)(acc[2] * rden), (half_t)(acc[3] * rden)});
   }
 }
 

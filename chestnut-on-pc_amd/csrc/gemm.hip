@@ -327,8 +327,9 @@ __device__ __forceinline__ void lds_barrier() {
 
 // Issue one K-step's loads of this wave into LDS stage `st` (A rows then B rows).
 // ko: the K-step's offset in A (halves); bko: in B (ko for a [N][K] B, ko
-// rows of ldb for a [K][N] B).
-template <int NIA, int NIB, int STAGE_A>
+// rows of ldb for a [K][N] B).  BPOL: the B loads' cache policy (0, or 2 =
+// non-temporal, see gemm_dma_kernel).
+template <int NIA, int NIB, int STAGE_A, int BPOL = 0>
 __device__ __forceinline__ void dma_issue(const half_t* const* asrc, const half_t* const* bsrc, half_t* st, int wave,
                                           int ko, long bko) {
 #pragma unroll
@@ -337,7 +338,7 @@ __device__ __forceinline__ void dma_issue(const half_t* const* asrc, const half_
 #pragma unroll
   for (int i = 0; i < NIB; ++i)
     __builtin_amdgcn_global_load_lds(bsrc[i] + bko, (lds_ptr_t)(st + STAGE_A + (wave * NIB + i) * 8 * BK), 16, 0,
-                                     0);
+                                     BPOL);
 }
 
 // Coalesced epilogue.  The MFMA accumulator layout gives a lane one column
@@ -349,11 +350,11 @@ __device__ __forceinline__ void dma_issue(const half_t* const* asrc, const half_
 // columns are staged transposed ([n][m]), four consecutive rows of a lane
 // forming one 8-byte LDS write, so V^T rows leave contiguously as well.
 // Row pitches carry 16 bytes of padding so the two half-waves' staging
-// writes (rows r and r+4) fall in different banks.  The split-K partials and
-// the row-major f16 outputs, read by the next kernel, leave with the
-// device-scope cache policy (store_sc1: -0.5% and -0.4% of the 1B frame
-// against non-temporal stores, which were themselves 0.9% ahead of default
-// stores); the f32 outputs with non-temporal stores.
+// writes (rows r and r+4) fall in different banks.  The split-K partials,
+// the row-major f16 outputs and the QKV fragments, read by the next kernel,
+// leave with the device-scope cache policy (store_sc1: -0.5%, -0.4% and
+// -0.3% of the 1B frame against non-temporal or default stores); the f32
+// outputs with non-temporal stores.
 // Requires (checked on the host, else the direct per-element stores run):
 // N % 8 == 0, ldc / batch stride / base of C and ws 16-byte compatible,
 // and for QKV qk_cols % BN == 0, M % 8 == 0 and vt_ld % 8 == 0.
@@ -453,7 +454,8 @@ __device__ __forceinline__ void store_staged(const GemmParams& p, const float16_
         const long chunk = ((cbase + cb) * tpb + (mw >> 5) + tb) * 64 + g * 16 + r;
         const half4_t lo = *reinterpret_cast<const half4_t*>(st + nl * PT + ml);
         const half4_t hi = *reinterpret_cast<const half4_t*>(st + nl * PT + ml + 16);
-        *reinterpret_cast<half8_t*>(p.vt + chunk * 8) = half8_t{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        store_sc1(sc1_rsrc(p.vt, 2L * p.M * (p.N - p.qk_cols)), chunk * 16,
+                  half8_t{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]});
       }
       return;
     }
@@ -499,8 +501,7 @@ __device__ __forceinline__ void store_staged(const GemmParams& p, const float16_
       if (mw + tb * 16 >= p.M) continue;
       const int ml = tb * 16 + r, nl = kb * 32 + g * 8;
       const long chunk = ((hbase + (mw >> 4) + tb) * kpb + (c0 >> 5) + kb) * 64 + g * 16 + r;
-      *reinterpret_cast<half8_t*>(static_cast<half_t*>(p.C) + chunk * 8) =
-          *reinterpret_cast<const half8_t*>(st + ml * PH + nl);
+      store_sc1(sc1_rsrc(p.C, 2L * p.M * p.qk_cols), chunk * 16, *reinterpret_cast<const half8_t*>(st + ml * PH + nl));
     }
     return;
   }
@@ -522,7 +523,7 @@ __device__ __forceinline__ void store_staged(const GemmParams& p, const float16_
 
 // Issue the load instructions [lo, hi) of a K-step (A rows first, then B
 // rows); lo and hi are compile-time after unrolling, so the untaken ones vanish.
-template <int NIA, int NIB, int STAGE_A>
+template <int NIA, int NIB, int STAGE_A, int BPOL = 0>
 __device__ __forceinline__ void dma_issue_range(const half_t* const* asrc, const half_t* const* bsrc, half_t* st,
                                                 int wave, int ko, long bko, int lo, int hi) {
 #pragma unroll
@@ -533,7 +534,7 @@ __device__ __forceinline__ void dma_issue_range(const half_t* const* asrc, const
   for (int i = 0; i < NIB; ++i)
     if (NIA + i >= lo && NIA + i < hi)
       __builtin_amdgcn_global_load_lds(bsrc[i] + bko, (lds_ptr_t)(st + STAGE_A + (wave * NIB + i) * 8 * BK), 16, 0,
-                                       0);
+                                       BPOL);
 }
 
 // Swizzle of a [K][N] B stage (rows of 128 halves = 16 chunks of 16 bytes):
@@ -568,6 +569,12 @@ __global__ __launch_bounds__(64 * NWG * KG) void gemm_dma_kernel(const GemmParam
   static_assert(S % KG == 0 && S / KG >= 2, "each K-group owns at least two ring stages");
   static_assert(KG == 1 || NWG == 4, "K-groups are built from 4-wave groups");
   constexpr int P = S / KG - 1;   // steps a group keeps in flight while it computes
+  // The B (weight) stream of the tiles with 128 or more rows -- the 1B model's
+  // block GEMMs, 8-34 MB of weights each -- is loaded non-temporal: -1.3% of
+  // the 1B frame.  Smaller tiles serve GEMMs whose few MB of weights the other
+  // workgroups reuse from the caches (the 39M model: +2.4% with it), and the
+  // [K][N] path keeps the default policy.
+  constexpr int BPOL = (BM >= 128 && !BT) ? 2 : 0;
   __shared__ __attribute__((aligned(1024))) half_t lds[S * STAGE];
   constexpr int WM = BM / (NWG / 2), WN = BN / 2;
   constexpr int FM = WM / 32, FN = WN / 32;
@@ -653,9 +660,9 @@ __global__ __launch_bounds__(64 * NWG * KG) void gemm_dma_kernel(const GemmParam
       if (CV) {
         const half_t* acv[NIA];
         conv_step(acv, KG * t + grp);
-        dma_issue<NIA, NIB, STAGE_A>(acv, bsrc, lds + (KG * t + grp) * STAGE, w4, 0, bko);
+        dma_issue<NIA, NIB, STAGE_A, BPOL>(acv, bsrc, lds + (KG * t + grp) * STAGE, w4, 0, bko);
       } else {
-        dma_issue<NIA, NIB, STAGE_A>(asrc, bsrc, lds + (KG * t + grp) * STAGE, w4, (KG * t + grp) * BK, bko);
+        dma_issue<NIA, NIB, STAGE_A, BPOL>(asrc, bsrc, lds + (KG * t + grp) * STAGE, w4, (KG * t + grp) * BK, bko);
       }
     }
 
@@ -735,7 +742,8 @@ __global__ __launch_bounds__(64 * NWG * KG) void gemm_dma_kernel(const GemmParam
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int kk = 0; kk < KS; ++kk) {
-      if (refill) dma_issue_range<NIA, NIB, STAGE_A>(ra, bsrc, rst, w4, rako, rbko, kk * NI / KS, (kk + 1) * NI / KS);
+      if (refill)
+        dma_issue_range<NIA, NIB, STAGE_A, BPOL>(ra, bsrc, rst, w4, rako, rbko, kk * NI / KS, (kk + 1) * NI / KS);
 #pragma unroll
       for (int i = 0; i < FM; ++i)
 #pragma unroll
