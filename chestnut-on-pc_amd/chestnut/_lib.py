@@ -42,6 +42,7 @@ _SIGS = {
     'ck_kernel_times': (c_int, [c_void_p, P(c_float), c_int]),
     'ck_run_range': (c_int, [c_void_p, c_int, c_int]),
     'ck_time_launches': (c_int, [c_void_p, P(c_int), c_int, c_int, P(c_float)]),
+    'ck_time_in_frames': (c_int, [c_void_p, P(c_int), c_int, c_int, P(c_float), P(c_float)]),
     'ck_tensor': (c_int, [c_void_p, c_char_p, P(c_void_p), P(c_size_t)]),
     'ck_state_count': (c_int, [c_void_p, P(c_int)]),
     'ck_decoded_layout': (c_int, [c_void_p, P(c_int), ctypes.c_char_p, c_size_t]),

@@ -1,12 +1,14 @@
 """BASELINE configs 1-3 as stand-alone workloads for timing and rocprofv3.
 
-    python -m chestnut.configs --config 1|2|3 [--reps N] [--out PATH]
+    python -m chestnut.configs --config 1|2|3 [--reps N] [--warmup-ms MS] [--out PATH]
 
 Each run first copies 256 MiB device to device (the calibration dispatch the
-FETCH_SIZE / WRITE_SIZE summaries scale by), then launches the config's
-kernels `reps` times over rotating copies of the operands, so the streamed
-bytes exceed the 256 MB Infinity Cache as in a real frame, and times them
-with HIP events on the launching stream.  It writes a JSON description (what
+FETCH_SIZE / WRITE_SIZE summaries scale by), runs the config's kernels
+untimed for --warmup-ms of GPU time (the GPU's clocks ramp up over the first
+tens of milliseconds of sustained load), then launches them `reps` times over
+rotating copies of the operands, so the streamed bytes exceed the 256 MB
+Infinity Cache as in a real frame, and times them with HIP events on the
+launching stream.  It writes a JSON description (what
 each launch is, its algorithmic flops and bytes, the event timing) that
 `python -m chestnut.profiling configs` joins with the kernel trace and the
 counter passes.
@@ -42,7 +44,27 @@ def calibration_copy(torch):
     del src, dst
 
 
-def config1(torch, reps):
+def warm(torch, fn, ms):
+    """Run fn() (one untimed repetition) until about `ms` of GPU time has
+    passed.  fn may return its own elapsed ms (work on another stream than
+    torch's); otherwise it is timed with events on torch's current stream.
+    At most 10,000 repetitions."""
+    if ms <= 0:
+        return 0
+    e0, e1 = _events(torch)
+    e0.record()
+    r = fn()
+    e1.record()
+    torch.cuda.synchronize()
+    one = r if isinstance(r, float) and r > 0 else e0.elapsed_time(e1)
+    n = min(int(ms / max(one, 1e-3)) + 1, 10000)
+    for _ in range(n):
+        fn()
+    torch.cuda.synchronize()
+    return n + 1
+
+
+def config1(torch, reps, warmup_ms=0):
     from . import kernels as K
     M, N, Kd = 1024, 1024, 6144
     copies = 12                       # 12 x 25 MB of operands > the 256 MB Infinity Cache
@@ -55,6 +77,7 @@ def config1(torch, reps):
     for a, b in zip(A, B):
         K.gemm(a, b, out=C, workspace=ws)
     torch.cuda.synchronize()
+    warm(torch, lambda: [K.gemm(a, b, out=C, workspace=ws) for a, b in zip(A, B)], warmup_ms)
     e0, e1 = _events(torch)
     e0.record()
     for r in range(reps):
@@ -71,7 +94,7 @@ def config1(torch, reps):
             'algorithmic': {'gemm': {'flops': flops, 'bytes': byts}}}
 
 
-def config2(torch, reps):
+def config2(torch, reps, warmup_ms=0):
     from . import kernels as K
     rows, Kd = 3072, 12288
     copies = 5                        # 5 x 75.5 MB > the 256 MB Infinity Cache
@@ -82,6 +105,7 @@ def config2(torch, reps):
     for w in W:
         K.gemv(w, x, out=y)
     torch.cuda.synchronize()
+    warm(torch, lambda: [K.gemv(w, x, out=y) for w in W], warmup_ms)
     e0, e1 = _events(torch)
     e0.record()
     for r in range(reps):
@@ -96,7 +120,7 @@ def config2(torch, reps):
             'algorithmic': {'gemv': {'flops': 2.0 * rows * Kd, 'bytes': byts}}}
 
 
-def config3(torch, reps):
+def config3(torch, reps, warmup_ms=0):
     from . import spec as S
     from .engine import Engine
     layers = 4                        # 4 x 100 MB of block weights > the 256 MB Infinity Cache
@@ -111,6 +135,7 @@ def config3(torch, reps):
         lo, hi = names.index('blk0.ln1'), names.index('final.ln')
         idx = list(range(lo, hi))      # every block's ln1 .. down (its ln1 adds the previous down's partials)
         eng.time_launches(idx, 1)
+        warm(torch, lambda: eng.time_launches(idx, 1), warmup_ms)
         ms = eng.time_launches(idx, reps)
         # one block = 7 plan entries; the first block's ln1 has no partials to add, so
         # the per-entry figures use block 1 (its ln1 adds block 0's MLP-down partials)
@@ -130,6 +155,8 @@ def main(argv=None):
     ap = argparse.ArgumentParser(prog='python -m chestnut.configs')
     ap.add_argument('--config', type=int, required=True, choices=(1, 2, 3))
     ap.add_argument('--reps', type=int, default=0, help='timed launches (default: 120 / 200 / 10)')
+    ap.add_argument('--warmup-ms', type=float, default=300.0,
+                    help='untimed repetitions for about this much GPU time before the timed ones')
     ap.add_argument('--out', default=None, help='write the run description as JSON')
     a = ap.parse_args(argv)
     import torch
@@ -138,7 +165,8 @@ def main(argv=None):
     calibration_copy(torch)
     t0 = time.perf_counter()
     reps = a.reps or {1: 120, 2: 200, 3: 10}[a.config]
-    res = {1: config1, 2: config2, 3: config3}[a.config](torch, reps)
+    res = {1: config1, 2: config2, 3: config3}[a.config](torch, reps, a.warmup_ms)
+    res['warmup_ms'] = a.warmup_ms
     res['copy_bytes'] = COPY_BYTES
     res['wall_s'] = round(time.perf_counter() - t0, 3)
     print(json.dumps(res), flush=True)

@@ -217,6 +217,18 @@ class Engine:
         call('ck_time_launches', self._h, idx, len(indices), int(reps), ctypes.byref(ms))
         return ms.value
 
+    def time_in_frames(self, indices, frames=5):
+        """Kernel time (ms) of plan entries `indices` inside `frames` whole
+        eager frames, from each kernel's own start and end timestamps: the
+        per-entry times per frame (a list) and their mean."""
+        if not indices:
+            raise ValueError('time_in_frames: no plan entries given')
+        idx = (ctypes.c_int * len(indices))(*indices)
+        per = (ctypes.c_float * len(indices))()
+        mean = ctypes.c_float()
+        call('ck_time_in_frames', self._h, idx, len(indices), int(frames), per, ctypes.byref(mean))
+        return list(per), mean.value
+
     # -- tensors ----------------------------------------------------------------
     def tensor_ptr(self, name):
         p = ctypes.c_void_p()

@@ -192,7 +192,7 @@ __global__ __launch_bounds__(64 * att_waves(NKT)) void attention_kernel(const ha
 template <int HD, int NKT, bool FRAG>
 void launch_t(int n_heads, const half_t* qk, const half_t* vt, half_t* out, float scale_log2e, hipStream_t s) {
   const dim3 grid((64 * NKT / ATT_QB) * n_heads);
-  hipLaunchKernelGGL((attention_kernel<HD, NKT, FRAG>), grid, dim3(64 * att_waves(NKT)), 0, s, qk, vt, out, n_heads,
+  CK_LAUNCH((attention_kernel<HD, NKT, FRAG>), grid, dim3(64 * att_waves(NKT)), 0, s, qk, vt, out, n_heads,
                      scale_log2e);
 }
 

@@ -252,6 +252,14 @@ int ck_time_launches(ck_engine* e, const int* idx, int n, int reps, float* ms) {
   CK_API_END
 }
 
+int ck_time_in_frames(ck_engine* e, const int* idx, int n, int frames, float* per_entry_ms, float* mean_ms) {
+  CK_API_BEGIN
+  CK_REQUIRE(e && idx && n > 0 && frames > 0, "ck_time_in_frames: bad arguments");
+  const float m = e->time_in_frames(idx, n, frames, per_entry_ms);
+  if (mean_ms) *mean_ms = m;
+  CK_API_END
+}
+
 int ck_tensor(ck_engine* e, const char* name, void** dptr, size_t* nbytes) {
   CK_API_BEGIN
   CK_REQUIRE(e && name, "null argument");

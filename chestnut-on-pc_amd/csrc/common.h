@@ -2,11 +2,14 @@
 // vector types, wave-level reductions and the image2d texel addressing rule.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
 #include <stdexcept>
 #include <string>
+#include <utility>
+#include <vector>
 
 namespace ck {
 
@@ -30,6 +33,33 @@ void set_last_error(const std::string& msg);
 
 // Launch check: a launch error (bad grid, invalid symbol) surfaces here.
 #define CK_LAUNCHED(what) CK_HIP(hipGetLastError())
+
+// In-frame kernel timing.  While `on` is set on this thread (eager launches
+// only, never under graph capture), every CK_LAUNCH goes through
+// hipExtLaunchKernelGGL with a start and a stop event, which receive the
+// dispatch's own begin and end timestamps -- the interval a kernel trace
+// reports, with no marker packet between the frame's kernels.  The caller
+// owns and destroys the recorded events.
+struct LaunchTimer {
+  bool on = false;
+  std::vector<std::pair<hipEvent_t, hipEvent_t>> events;
+};
+LaunchTimer& launch_timer();
+
+#define CK_LAUNCH(kernel, grid, block, shmem, stream, ...)                                      \
+  do {                                                                                          \
+    ::ck::LaunchTimer& ck_lt_ = ::ck::launch_timer();                                           \
+    if (ck_lt_.on) {                                                                            \
+      hipEvent_t ck_e0_ = nullptr, ck_e1_ = nullptr;                                            \
+      CK_HIP(hipEventCreate(&ck_e0_));                                                          \
+      ck_lt_.events.emplace_back(ck_e0_, nullptr);                                              \
+      CK_HIP(hipEventCreate(&ck_e1_));                                                          \
+      ck_lt_.events.back().second = ck_e1_;                                                     \
+      hipExtLaunchKernelGGL(kernel, grid, block, shmem, stream, ck_e0_, ck_e1_, 0, __VA_ARGS__); \
+    } else {                                                                                    \
+      hipLaunchKernelGGL(kernel, grid, block, shmem, stream, __VA_ARGS__);                      \
+    }                                                                                           \
+  } while (0)
 
 typedef _Float16 half_t;
 typedef _Float16 half4_t __attribute__((ext_vector_type(4)));

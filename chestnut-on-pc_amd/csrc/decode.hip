@@ -141,7 +141,7 @@ void launch_decode(const float* raw, float* decoded, const DecodeHead* heads_dev
                    unsigned* counter, const float* h, float* packed_feat, int H) {
   CK_REQUIRE(raw && decoded && heads_dev && n_heads > 0, "decode: bad arguments");
   CK_REQUIRE(!counter || (h && packed_feat && H > 0), "decode: the frame tick needs h, packed_feat and H");
-  hipLaunchKernelGGL(decode_kernel, dim3(n_heads + (counter ? 1 : 0)), dim3(256), 0, s, raw, decoded, heads_dev,
+  CK_LAUNCH(decode_kernel, dim3(n_heads + (counter ? 1 : 0)), dim3(256), 0, s, raw, decoded, heads_dev,
                      n_heads, counter, h, packed_feat, H);
   CK_LAUNCHED("decode");
 }

@@ -121,6 +121,11 @@ Spec parse_spec(const std::string& json) {
   return s;
 }
 
+LaunchTimer& launch_timer() {
+  static thread_local LaunchTimer t;
+  return t;
+}
+
 }  // namespace ck
 
 using namespace ck;
@@ -726,16 +731,38 @@ void ck_engine::drop_graph() {
 // engine stream waits for the side stream at the next entry marked `join`
 // (or at the end).  The same calls serve eager frames and graph capture,
 // where the fork and join become graph edges.
-void ck_engine::launch_plan() {
+void ck_engine::launch_plan(const std::vector<char>* timed,
+                            std::vector<std::vector<std::pair<hipEvent_t, hipEvent_t>>>* events) {
   bool forked = false, pending = false;
-  for (auto& l : plan) {
+  LaunchTimer& lt = launch_timer();
+  auto run = [&](size_t i, hipStream_t s) {
+    if (!timed || !(*timed)[i]) {
+      plan[i].fn(s);
+      return;
+    }
+    lt.events.clear();
+    lt.on = true;
+    try {
+      plan[i].fn(s);
+    } catch (...) {
+      lt.on = false;
+      for (auto& e : lt.events) (*events)[i].push_back(e);
+      lt.events.clear();
+      throw;
+    }
+    lt.on = false;
+    for (auto& e : lt.events) (*events)[i].push_back(e);
+    lt.events.clear();
+  };
+  for (size_t i = 0; i < plan.size(); ++i) {
+    const Launch& l = plan[i];
     if (l.branch) {
       if (!forked) {
         CK_HIP(hipEventRecord(ev_fork, stream));
         CK_HIP(hipStreamWaitEvent(side, ev_fork, 0));
         forked = true;
       }
-      l.fn(side);
+      run(i, side);
       pending = true;
       continue;
     }
@@ -744,7 +771,7 @@ void ck_engine::launch_plan() {
       CK_HIP(hipStreamWaitEvent(stream, ev_join, 0));
       pending = false;
     }
-    l.fn(stream);
+    run(i, stream);
   }
   if (pending) {
     CK_HIP(hipEventRecord(ev_join, side));
@@ -848,6 +875,51 @@ void ck_engine::kernel_times(float* ms, int n) {
   }
   (void)hipEventDestroy(e0);
   (void)hipEventDestroy(e1);
+}
+
+// Kernel time of plan entries inside whole frames: `frames` eager frames of
+// the full plan run back to back with no synchronisation between launches,
+// and the entries listed in idx are launched with start/stop events (each
+// kernel's own dispatch timestamps, see LaunchTimer).  per_entry_ms[k] = the
+// kernel time of entry idx[k] per frame (an entry with a split-K reduce
+// counts both kernels); returns the mean over the listed entries.
+float ck_engine::time_in_frames(const int* idx, int n, int frames, float* per_entry_ms) {
+  CK_REQUIRE(n > 0 && frames > 0, "time_in_frames: n and frames must be positive");
+  std::vector<char> timed(plan.size(), 0);
+  for (int k = 0; k < n; ++k) {
+    CK_REQUIRE(idx[k] >= 0 && idx[k] < (int)plan.size(), "time_in_frames: plan index out of range");
+    timed[idx[k]] = 1;
+  }
+  std::vector<std::vector<std::pair<hipEvent_t, hipEvent_t>>> events(plan.size());
+  auto destroy = [&]() {
+    for (auto& v : events)
+      for (auto& e : v) {
+        if (e.first) (void)hipEventDestroy(e.first);
+        if (e.second) (void)hipEventDestroy(e.second);
+      }
+  };
+  float total = 0.f;
+  try {
+    CK_HIP(hipStreamSynchronize(stream));
+    for (int f = 0; f < frames; ++f) launch_plan(&timed, &events);
+    CK_HIP(hipStreamSynchronize(stream));
+    if (side) CK_HIP(hipStreamSynchronize(side));
+    for (int k = 0; k < n; ++k) {
+      float sum = 0.f;
+      for (auto& e : events[idx[k]]) {
+        float ms = 0.f;
+        CK_HIP(hipEventElapsedTime(&ms, e.first, e.second));
+        sum += ms;
+      }
+      if (per_entry_ms) per_entry_ms[k] = sum / frames;
+      total += sum / frames;
+    }
+  } catch (...) {
+    destroy();
+    throw;
+  }
+  destroy();
+  return total / n;
 }
 
 float ck_engine::time_launches(const int* idx, int n, int reps) {

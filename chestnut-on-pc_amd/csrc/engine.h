@@ -93,13 +93,17 @@ struct ck_engine {
   void run_frame_nv12(const uint8_t* frame, const uint8_t* big_frame, const float* tfm, const float* big_tfm,
                       const float* packed, float* out);
   void frame_launch();
-  void launch_plan();
+  // timed: per plan entry, 1 = launch it with start/stop events appended to
+  // events[i] (see LaunchTimer); null for plain launches and graph capture
+  void launch_plan(const std::vector<char>* timed = nullptr,
+                   std::vector<std::vector<std::pair<hipEvent_t, hipEvent_t>>>* events = nullptr);
   void capture();
   void drop_graph();
   void reset_state();
   void run_range(int first, int last);
   void kernel_times(float* ms, int n);
   float time_launches(const int* idx, int n, int reps);
+  float time_in_frames(const int* idx, int n, int frames, float* per_entry_ms);
 
  private:
   void init();

@@ -864,8 +864,8 @@ void launch_dma_tile(const GemmParams& p, bool kg2, hipStream_t s) {
   constexpr int stage_bytes = (BM + BN) * BK * 2;
   constexpr int S1 = (5 * stage_bytes <= 163840) ? 5 : 4;
   constexpr int S2 = (BM == 64 && BN == 64) ? 4 : (6 * stage_bytes <= 163840 ? 6 : 4);
-  if (kg2) hipLaunchKernelGGL((gemm_dma_kernel<BM, BN, S2, 2, EPI>), dim3(grid), dim3(512), 0, s, p);
-  else hipLaunchKernelGGL((gemm_dma_kernel<BM, BN, S1, 1, EPI>), dim3(grid), dim3(256), 0, s, p);
+  if (kg2) CK_LAUNCH((gemm_dma_kernel<BM, BN, S2, 2, EPI>), dim3(grid), dim3(512), 0, s, p);
+  else CK_LAUNCH((gemm_dma_kernel<BM, BN, S1, 1, EPI>), dim3(grid), dim3(256), 0, s, p);
   CK_LAUNCHED("gemm_dma");
 }
 
@@ -876,8 +876,8 @@ void launch_dma_tile_cv(const GemmParams& p, bool kg2, hipStream_t s) {
   constexpr int stage_bytes = (BM + BN) * BK * 2;
   constexpr int S1 = (5 * stage_bytes <= 163840) ? 5 : 4;
   constexpr int S2 = (BM == 64 && BN == 64) ? 4 : (6 * stage_bytes <= 163840 ? 6 : 4);
-  if (kg2) hipLaunchKernelGGL((gemm_dma_kernel<BM, BN, S2, 2, EPI, 4, false, true>), dim3(grid), dim3(512), 0, s, p);
-  else hipLaunchKernelGGL((gemm_dma_kernel<BM, BN, S1, 1, EPI, 4, false, true>), dim3(grid), dim3(256), 0, s, p);
+  if (kg2) CK_LAUNCH((gemm_dma_kernel<BM, BN, S2, 2, EPI, 4, false, true>), dim3(grid), dim3(512), 0, s, p);
+  else CK_LAUNCH((gemm_dma_kernel<BM, BN, S1, 1, EPI, 4, false, true>), dim3(grid), dim3(256), 0, s, p);
   CK_LAUNCHED("gemm_dma_conv");
 }
 
@@ -896,8 +896,8 @@ void launch_epi_cv(int tile, const GemmParams& p, hipStream_t s) {
 // 128x128 LDS-DMA tile for a [K][N] B (f32 output), two K-groups (tile 1) or one.
 void launch_dma_bt(const GemmParams& p, bool kg2, hipStream_t s) {
   const int grid = p.Mt * p.Nt * p.split * p.batch;
-  if (kg2) hipLaunchKernelGGL((gemm_dma_kernel<128, 128, 4, 2, EPI_F32, 4, true>), dim3(grid), dim3(512), 0, s, p);
-  else hipLaunchKernelGGL((gemm_dma_kernel<128, 128, 5, 1, EPI_F32, 4, true>), dim3(grid), dim3(256), 0, s, p);
+  if (kg2) CK_LAUNCH((gemm_dma_kernel<128, 128, 4, 2, EPI_F32, 4, true>), dim3(grid), dim3(512), 0, s, p);
+  else CK_LAUNCH((gemm_dma_kernel<128, 128, 5, 1, EPI_F32, 4, true>), dim3(grid), dim3(256), 0, s, p);
   CK_LAUNCHED("gemm_dma_bt");
 }
 
@@ -905,14 +905,14 @@ void launch_dma_bt(const GemmParams& p, bool kg2, hipStream_t s) {
 template <int EPI>
 void launch_dma_tile8(const GemmParams& p, hipStream_t s) {
   const int grid = p.Mt * p.Nt * p.split * p.batch;
-  hipLaunchKernelGGL((gemm_dma_kernel<256, 128, 3, 1, EPI, 8>), dim3(grid), dim3(512), 0, s, p);
+  CK_LAUNCH((gemm_dma_kernel<256, 128, 3, 1, EPI, 8>), dim3(grid), dim3(512), 0, s, p);
   CK_LAUNCHED("gemm_dma");
 }
 
 template <int BM, int BN, bool BKN, int EPI>
 void launch_tile(const GemmParams& p, hipStream_t s) {
   const int grid = p.Mt * p.Nt * p.split * p.batch;
-  hipLaunchKernelGGL((gemm_kernel<BM, BN, BKN, EPI>), dim3(grid), dim3(256), 0, s, p);
+  CK_LAUNCH((gemm_kernel<BM, BN, BKN, EPI>), dim3(grid), dim3(256), 0, s, p);
   CK_LAUNCHED("gemm");
 }
 
@@ -951,7 +951,7 @@ template <int EPI>
 void launch_reduce(const GemmParams& p, hipStream_t s) {
   const long n = (long)p.M * p.N * p.batch / ((p.N & 3) == 0 ? 4 : 1);
   CK_REQUIRE((reinterpret_cast<uintptr_t>(p.ws) & 15) == 0, "gemm: split-K workspace must be 16-byte aligned");
-  hipLaunchKernelGGL(splitk_reduce_kernel<EPI>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, p);
+  CK_LAUNCH(splitk_reduce_kernel<EPI>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, p);
   CK_LAUNCHED("splitk_reduce");
 }
 
@@ -1107,7 +1107,7 @@ void launch_gemm(GemmDesc d, hipStream_t s) {
     const size_t partials = (d.split > 1) ? (size_t)d.split * d.batch * d.M * d.N : 0;
     half_t* bt = reinterpret_cast<half_t*>(d.ws + partials);
     CK_REQUIRE((reinterpret_cast<uintptr_t>(bt) & 15) == 0, "gemm: workspace must be 16-byte aligned");
-    hipLaunchKernelGGL(transpose_kn_kernel, dim3(d.K / 64, ceil_div(d.N, 64), d.batch), dim3(256), 0, s, d.B, d.ldb,
+    CK_LAUNCH(transpose_kn_kernel, dim3(d.K / 64, ceil_div(d.N, 64), d.batch), dim3(256), 0, s, d.B, d.ldb,
                        d.sB, bt, (long)d.N * d.K, d.K, d.N);
     CK_LAUNCHED("transpose_kn");
     p.B = bt;

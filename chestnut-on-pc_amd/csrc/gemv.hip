@@ -214,7 +214,7 @@ void launch_n(GemvArgs a0, GemvArgs a1, bool two, hipStream_t s) {
   } else {
     a1 = a0;
   }
-  hipLaunchKernelGGL((gemv_kernel<NSTEP, GATE>), dim3(grid), dim3(GEMV_THREADS), 0, s, a0, a1, nb0);
+  CK_LAUNCH((gemv_kernel<NSTEP, GATE>), dim3(grid), dim3(GEMV_THREADS), 0, s, a0, a1, nb0);
   CK_LAUNCHED("gemv");
 }
 

@@ -164,8 +164,8 @@ void ln_row_launch(float* x, const float* ws, int nsplit, long sstride, const fl
   dim3 grid(rows);
   auto go = [&](auto ns) {
     constexpr int NS = decltype(ns)::value;
-    if (f16) hipLaunchKernelGGL((layernorm_row_kernel<EPT, true, NS>), grid, dim3(256), 0, s, x, ws, nsplit, sstride, rbias, g, b, out, eps);
-    else hipLaunchKernelGGL((layernorm_row_kernel<EPT, false, NS>), grid, dim3(256), 0, s, x, ws, nsplit, sstride, rbias, g, b, out, eps);
+    if (f16) CK_LAUNCH((layernorm_row_kernel<EPT, true, NS>), grid, dim3(256), 0, s, x, ws, nsplit, sstride, rbias, g, b, out, eps);
+    else CK_LAUNCH((layernorm_row_kernel<EPT, false, NS>), grid, dim3(256), 0, s, x, ws, nsplit, sstride, rbias, g, b, out, eps);
   };
   if (!ws) go(std::integral_constant<int, 0>{});
   else if (nsplit == 1) go(std::integral_constant<int, 1>{});
@@ -180,11 +180,11 @@ void ln_launch(float* x, const float* ws, int nsplit, long sstride, const float*
                void* out, bool f16, int rows, float eps, hipStream_t s) {
   dim3 grid((rows + 3) / 4);
   if (ws) {
-    if (f16) hipLaunchKernelGGL((layernorm_kernel<EPL, true, true>), grid, dim3(256), 0, s, x, ws, nsplit, sstride, rbias, g, b, out, rows, eps);
-    else hipLaunchKernelGGL((layernorm_kernel<EPL, false, true>), grid, dim3(256), 0, s, x, ws, nsplit, sstride, rbias, g, b, out, rows, eps);
+    if (f16) CK_LAUNCH((layernorm_kernel<EPL, true, true>), grid, dim3(256), 0, s, x, ws, nsplit, sstride, rbias, g, b, out, rows, eps);
+    else CK_LAUNCH((layernorm_kernel<EPL, false, true>), grid, dim3(256), 0, s, x, ws, nsplit, sstride, rbias, g, b, out, rows, eps);
   } else {
-    if (f16) hipLaunchKernelGGL((layernorm_kernel<EPL, true, false>), grid, dim3(256), 0, s, x, ws, nsplit, sstride, rbias, g, b, out, rows, eps);
-    else hipLaunchKernelGGL((layernorm_kernel<EPL, false, false>), grid, dim3(256), 0, s, x, ws, nsplit, sstride, rbias, g, b, out, rows, eps);
+    if (f16) CK_LAUNCH((layernorm_kernel<EPL, true, false>), grid, dim3(256), 0, s, x, ws, nsplit, sstride, rbias, g, b, out, rows, eps);
+    else CK_LAUNCH((layernorm_kernel<EPL, false, false>), grid, dim3(256), 0, s, x, ws, nsplit, sstride, rbias, g, b, out, rows, eps);
   }
   CK_LAUNCHED("layernorm");
 }
@@ -260,13 +260,13 @@ void launch_colmean(const float* x, float* out, int rows, int d, hipStream_t s) 
   CK_REQUIRE(x && out && rows > 0 && d > 0, "colmean: bad arguments");
   CK_REQUIRE(d % COLMEAN_COLS == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0,
              "colmean: d must be a multiple of 32 and x 16-byte aligned");
-  hipLaunchKernelGGL(colmean_kernel, dim3(d / COLMEAN_COLS), dim3(256), 0, s, x, out, rows, d);
+  CK_LAUNCH(colmean_kernel, dim3(d / COLMEAN_COLS), dim3(256), 0, s, x, out, rows, d);
   CK_LAUNCHED("colmean");
 }
 
 void launch_fill_u32(void* p, unsigned v, size_t n_words, hipStream_t s) {
   if (n_words == 0) return;
-  hipLaunchKernelGGL(fill_u32_kernel, dim3((unsigned)((n_words + 255) / 256)), dim3(256), 0, s,
+  CK_LAUNCH(fill_u32_kernel, dim3((unsigned)((n_words + 255) / 256)), dim3(256), 0, s,
                      static_cast<unsigned*>(p), v, n_words);
   CK_LAUNCHED("fill_u32");
 }

@@ -160,7 +160,7 @@ struct alignas(sizeof(E) * LANES) Texel {
 
 template <typename TexelT>
 void gather_launch(const void* img, int A, int B, const int* yx, int n, void* out, hipStream_t s) {
-  hipLaunchKernelGGL(img_gather_kernel<TexelT>, dim3(ceil_div(n, 256)), dim3(256), 0, s,
+  CK_LAUNCH(img_gather_kernel<TexelT>, dim3(ceil_div(n, 256)), dim3(256), 0, s,
                      static_cast<const TexelT*>(img), A, B, yx, n, static_cast<TexelT*>(out));
   CK_LAUNCHED("img_gather");
 }
@@ -264,7 +264,7 @@ void launch_policy_inputs(const QueueDims& q, const uint8_t* warped, const float
   a.n_des = q.desire_hist * q.desire_len;
   a.n_des_push = q.desire_len;
   const long total = (long)a.n_img + a.n_feat + a.n_feat_push + a.n_des + a.n_des_push + 4;
-  hipLaunchKernelGGL(policy_inputs_kernel, dim3(ceil_div(total, 256)), dim3(256), 0, s, a);
+  CK_LAUNCH(policy_inputs_kernel, dim3(ceil_div(total, 256)), dim3(256), 0, s, a);
   CK_LAUNCHED("policy_inputs");
 }
 
@@ -272,7 +272,7 @@ void launch_yuv_to_channels(const uint8_t* Y, const uint8_t* U, const uint8_t* V
                             hipStream_t s) {
   CK_REQUIRE(Y && U && V && out, "yuv_to_channels: null pointer");
   CK_REQUIRE(H > 0 && W > 0 && H % 2 == 0 && W % 2 == 0, "yuv_to_channels: H and W must be positive and even");
-  hipLaunchKernelGGL(yuv_to_channels_kernel, dim3(ceil_div((long)(H / 2) * (W / 2), 256)), dim3(256), 0, s, Y, U, V,
+  CK_LAUNCH(yuv_to_channels_kernel, dim3(ceil_div((long)(H / 2) * (W / 2), 256)), dim3(256), 0, s, Y, U, V,
                      H, W, out);
   CK_LAUNCHED("yuv_to_channels");
 }
@@ -280,7 +280,7 @@ void launch_yuv_to_channels(const uint8_t* Y, const uint8_t* U, const uint8_t* V
 void launch_i420_to_channels(const uint8_t* frame, int H, int W, uint8_t* out, hipStream_t s) {
   CK_REQUIRE(frame && out, "i420_to_channels: null pointer");
   CK_REQUIRE(H > 0 && W > 0 && H % 4 == 0 && W % 2 == 0, "i420_to_channels: H must be a multiple of 4, W even");
-  hipLaunchKernelGGL(i420_to_channels_kernel, dim3(ceil_div((long)(H / 2) * (W / 2), 256)), dim3(256), 0, s, frame,
+  CK_LAUNCH(i420_to_channels_kernel, dim3(ceil_div((long)(H / 2) * (W / 2), 256)), dim3(256), 0, s, frame,
                      H, W, out);
   CK_LAUNCHED("i420_to_channels");
 }
@@ -310,7 +310,7 @@ void launch_im2col_u8(const uint8_t* img, int batch, int C, int H, int W, half_t
   const int Ho = (H - 1) / 2 + 1, Wo = (W - 1) / 2 + 1;
   const long per = (long)Ho * Wo * (Kp / 8);
   CK_REQUIRE(per < (1L << 31) && (long)H * W < (1L << 31), "im2col_u8: image too large");
-  hipLaunchKernelGGL(im2col_u8_kernel, dim3(ceil_div(per, 256), batch), dim3(256), 0, s, img, C, H, W, patches, Kp,
+  CK_LAUNCH(im2col_u8_kernel, dim3(ceil_div(per, 256), batch), dim3(256), 0, s, img, C, H, W, patches, Kp,
                      Ho, Wo);
   CK_LAUNCHED("im2col_u8");
 }
@@ -321,13 +321,13 @@ void launch_im2col_f16(const half_t* act, int batch, int C, int H, int W, half_t
   const int Ho = (H - 1) / 2 + 1, Wo = (W - 1) / 2 + 1;
   const long per = (long)Ho * Wo * (Kp / 4);
   CK_REQUIRE(per < (1L << 31), "im2col_f16: image too large");
-  hipLaunchKernelGGL(im2col_f16_kernel, dim3(ceil_div(per, 256), batch), dim3(256), 0, s, act, C, H, W, patches, Kp,
+  CK_LAUNCH(im2col_f16_kernel, dim3(ceil_div(per, 256), batch), dim3(256), 0, s, act, C, H, W, patches, Kp,
                      Ho, Wo);
   CK_LAUNCHED("im2col_f16");
 }
 
 void launch_tokens(const half_t* stem_out, int n_spatial, int C5, half_t* F, hipStream_t s) {
-  hipLaunchKernelGGL(tokens_kernel, dim3(ceil_div(2L * n_spatial * C5, 256)), dim3(256), 0, s, stem_out, n_spatial,
+  CK_LAUNCH(tokens_kernel, dim3(ceil_div(2L * n_spatial * C5, 256)), dim3(256), 0, s, stem_out, n_spatial,
                      C5, F);
   CK_LAUNCHED("tokens");
 }

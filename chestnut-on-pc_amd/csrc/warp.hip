@@ -82,7 +82,7 @@ void launch_warp_nv12(const uint8_t* frame, const uint8_t* big_frame, size_t fra
   CK_REQUIRE((size_t)(uv_offset + (long)(cam_h / 2) * stride) <= frame_bytes,
              "warp_nv12: frame buffer smaller than its Y plane and the UV rows the warp reads");
   const long n = 2L * (model_h / 2) * (model_w / 2);
-  hipLaunchKernelGGL(warp_nv12_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, frame, big_frame, tfm,
+  CK_LAUNCH(warp_nv12_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, frame, big_frame, tfm,
                      big_tfm, cam_w, cam_h, stride, uv_offset, model_w, model_h, out);
   CK_LAUNCHED("warp_nv12");
 }

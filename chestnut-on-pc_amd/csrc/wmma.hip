@@ -82,14 +82,14 @@ __global__ __launch_bounds__(64) void mfma_kat_kernel(int variant, const uint16_
 void launch_wmma_rdna4(const uint16_t* fa, const uint16_t* fb, const float* fc, float* fd, int n_tiles,
                        hipStream_t s) {
   CK_REQUIRE(fa && fb && fc && fd && n_tiles > 0, "wmma_rdna4: bad arguments");
-  hipLaunchKernelGGL(wmma_rdna4_kernel, dim3(n_tiles), dim3(64), 0, s, fa, fb, fc, fd);
+  CK_LAUNCH(wmma_rdna4_kernel, dim3(n_tiles), dim3(64), 0, s, fa, fb, fc, fd);
   CK_LAUNCHED("wmma_rdna4");
 }
 
 void launch_mfma_kat(int variant, const uint16_t* A, const uint16_t* B, float* D, hipStream_t s) {
   CK_REQUIRE(A && B && D, "mfma_kat: null pointer");
   CK_REQUIRE(variant == 0 || variant == 1, "mfma_kat: variant must be 0 (16x16x32) or 1 (32x32x16)");
-  hipLaunchKernelGGL(mfma_kat_kernel, dim3(1), dim3(64), 0, s, variant, A, B, D);
+  CK_LAUNCH(mfma_kat_kernel, dim3(1), dim3(64), 0, s, variant, A, B, D);
   CK_LAUNCHED("mfma_kat");
 }
 

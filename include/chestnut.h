@@ -131,6 +131,15 @@ int ck_run_range(ck_engine* e, int first, int last);
  * Replaces: the per-kernel bench loop of bench_r62.py:25-37. */
 int ck_time_launches(ck_engine* e, const int* idx, int n, int reps, float* ms);
 
+/* Run `frames` whole eager frames back to back (no synchronisation between
+ * launches, the frame's state advancing as usual) and time the kernels of
+ * plan entries idx[0..n) by their own dispatch start and end timestamps:
+ * per_entry_ms[k] = entry idx[k]'s kernel time per frame (may be NULL),
+ * *mean_ms = the mean over the n entries (may be NULL).  The in-frame
+ * duration a kernel trace reports, measured without a profiler.
+ * Replaces: KTIME=1, per-kernel GPU time over a run (run_pinned2.py:1307-1329). */
+int ck_time_in_frames(ck_engine* e, const int* idx, int n, int frames, float* per_entry_ms, float* mean_ms);
+
 /* Named device tensors (parameters, inputs, queue rings, activations):
  * device pointer + logical size, and synchronous host copies.
  * Replaces: KDUMP pre-state dumps (run_pinned2.py:1533-1545) and the

@@ -194,6 +194,40 @@ def test_kernel_times_cover_plan(tiny):
     assert names[0] == 'inputs' and names[-1] == 'decode' and 'blk0.qkv' in names
 
 
+def test_time_in_frames_leaves_frames_unchanged(tiny):
+    """In-frame kernel timing runs whole eager frames: every plan entry gets a
+    positive kernel time, their sum stays below the frames' wall time, and the
+    timed frames compute exactly what plain eager frames compute."""
+    import time
+    sp, w, eng = tiny
+    n = len(eng.plan())
+    rng = np.random.default_rng(15)
+    warped, packed = next(frame_inputs(rng, sp, 1))
+    results = []
+    for timed in (False, True):
+        eng.reset()
+        eng.set_graph(False)
+        eng.write('warped', warped)
+        eng.write('packed', packed)
+        if timed:
+            t0 = time.perf_counter()
+            per, mean = eng.time_in_frames(list(range(n)), frames=3)
+            wall_ms = (time.perf_counter() - t0) * 1e3
+            assert len(per) == n and all(x > 0 for x in per), per
+            assert abs(mean - sum(per) / n) <= 1e-6 * max(1.0, mean)
+            assert 3 * sum(per) <= wall_ms, (sum(per), wall_ms)
+        else:
+            for _ in range(3):
+                eng.frame_launch()
+            eng.synchronize()
+        results.append((eng.read('out', np.float32), eng.read('x', np.float32)))
+    eng.set_graph(True)
+    for a, b in zip(*results):
+        np.testing.assert_array_equal(a, b)
+    with pytest.raises(RuntimeError, match='plan index out of range'):
+        eng.time_in_frames([n], frames=1)
+
+
 def test_config3_single_block(gpu):
     """one d=2048, 16x128, T=512, MLP 8192 pre-LN block,
     x ~ N(0,1); injected into the plan's residual and run alone."""
