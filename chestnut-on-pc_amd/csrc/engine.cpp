@@ -450,6 +450,14 @@ void ck_engine::build_plan() {
   plan.clear();
   const int d = sp.d, F = sp.d_ff, Hh = sp.hidden, dl = sp.desire_len;
   const long HW = (long)sp.img_h * sp.img_w;
+  // The GEMVs load their weights non-temporally unless the whole model's
+  // parameters fit comfortably in the 256 MB Infinity Cache, where the
+  // default policy keeps them from one frame to the next (39M model: -1.1%
+  // per frame; the 1B model's 2 GB stream either way and gain from it).
+  size_t param_bytes = 0;
+  for (const auto& t : tensors)
+    if (t.param) param_bytes += t.nbytes;
+  const bool stream_w = param_bytes > (size_t(128) << 20);
   auto h16 = [&](const std::string& n) { return static_cast<half_t*>(ptr(n)); };
   auto f32 = [&](const std::string& n) { return static_cast<float*>(ptr(n)); };
 
@@ -482,7 +490,7 @@ void ck_engine::build_plan() {
     const float* fbuf = f32("feat_buf");
     float* cin = f32("ctx_in");
     add("temporal", "gemv", 2.0 * Td * Kt, (double)Td * Kt * 2 + Kt * 4 + Td * 8, [=](hipStream_t s) {
-      launch_gemv(tw, fbuf, tb, cin, Td, Kt, Kt, GEMV_GELU, 0, s);
+      launch_gemv(tw, fbuf, tb, cin, Td, Kt, Kt, GEMV_GELU, 0, s, stream_w);
     });
     plan.back().branch = branch;
     const half_t* cw = h16("ctx.w");
@@ -490,7 +498,7 @@ void ck_engine::build_plan() {
     float* ctx = f32("ctx");
     const int ldc = ld_ctx;
     add("context", "gemv", 2.0 * d * ldc, (double)d * ldc * 2 + ldc * 4 + d * 8, [=](hipStream_t s) {
-      launch_gemv(cw, cin, cb, ctx, d, ldc, ldc, GEMV_NONE, 0, s);
+      launch_gemv(cw, cin, cb, ctx, d, ldc, ldc, GEMV_NONE, 0, s, stream_w);
     });
     plan.back().branch = branch;
   };
@@ -678,7 +686,7 @@ void ck_engine::build_plan() {
     const float* bhh = f32("gru.bhh");
     // gi = W_ih pooled + b_ih and gh = W_hh h_prev + b_hh: one launch
     add("gru", "gemv2", 2.0 * 3 * Hh * (d + Hh), 3.0 * Hh * (d + Hh) * 2, [=](hipStream_t s) {
-      launch_gemv2(wih, pooled, bih, gi, 3 * Hh, d, whh, hprev, bhh, gh, 3 * Hh, Hh, s);
+      launch_gemv2(wih, pooled, bih, gi, 3 * Hh, d, whh, hprev, bhh, gh, 3 * Hh, Hh, s, stream_w);
     });
     // heads on the new hidden state; the GRU update is computed inside the
     // GEMV, which also stores h to h_new and to the output's hidden_state slice
@@ -688,7 +696,7 @@ void ck_engine::build_plan() {
     const half_t* hw = h16("head.w");
     const float* hbias = f32("head.b");
     add("heads", "gemv_gru", 2.0 * nho * Hh, (double)nho * Hh * 2 + 7.0 * Hh * 4, [=](hipStream_t s) {
-      launch_gemv_gru(hw, hbias, out, nho, gi, gh, hprev, hn, out + nho, Hh, s);
+      launch_gemv_gru(hw, hbias, out, nho, gi, gh, hprev, hn, out + nho, Hh, s, stream_w);
     });
     // the Parser's decode, and in the same launch the end-of-frame tick:
     // queue counter + 1, h_new -> packed prev_feat (read by the next frame)

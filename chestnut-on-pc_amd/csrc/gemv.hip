@@ -8,10 +8,13 @@
 //     2048-column step, and keeps its slice of x in registers for all rows;
 //   * every W read is one 16-byte load per lane, fully coalesced (a wave
 //     reads 1 KiB contiguous per instruction); RB rows are loaded before any
-//     arithmetic so each lane has RB*NSTEP loads in flight.  W is read once
-//     per frame and never again, so the loads are non-temporal (they do not
-//     displace x and the activations from the caches), which measures
-//     ~6% faster on the config-2 shape;
+//     arithmetic so each lane has RB*NSTEP loads in flight.  For weights that
+//     stream (the config-2 shape, the 1B model's 2 GB) the loads are
+//     non-temporal: they do not displace x and the activations from the
+//     caches (config 2: 13.8 against 15.0 us).  A model whose weights fit the
+//     256 MB Infinity Cache (the 39M model) loads them with the default policy
+//     and finds them there the next frame (-1.1% of its frame); the caller
+//     chooses (`stream`);
 //   * workgroups are small (one 4-row batch each for up to 4096 rows): three
 //     or more resident per CU keep more requests in flight than a few long
 //     workgroups would (3072 rows: 768 workgroups);
@@ -56,7 +59,7 @@ struct GemvArgs {
   float* h2;
 };
 
-template <int NSTEP, bool GATE>
+template <int NSTEP, bool GATE, bool NT>
 __global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(const GemvArgs a0, const GemvArgs a1, int nb0) {
   __shared__ float red[2][4][GEMV_RB];
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
@@ -86,12 +89,14 @@ __global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(const GemvArgs a0, c
           // columns past K re-read the row's last chunk (in bounds, finite)
           // and meet x = 0, adding exact zeros: without a branch the gate
           // loads and arithmetic need not wait for these loads
-          w[i][s] = __builtin_nontemporal_load(reinterpret_cast<const half8_t*>(wr + min(c, K - 8)));
+          const half8_t* p = reinterpret_cast<const half8_t*>(wr + min(c, K - 8));
+          w[i][s] = NT ? __builtin_nontemporal_load(p) : *p;
         } else if (c < K) {
           // the branch keeps every load of the batch ahead of the first FMA
           // (branch-free, the compiler interleaves loads with the FMAs and
           // holds about 2 in flight per lane instead of RB*NSTEP)
-          w[i][s] = __builtin_nontemporal_load(reinterpret_cast<const half8_t*>(wr + c));
+          const half8_t* p = reinterpret_cast<const half8_t*>(wr + c);
+          w[i][s] = NT ? __builtin_nontemporal_load(p) : *p;
         } else {
           w[i][s] = half8_t{};
         }
@@ -204,7 +209,7 @@ int batch_rows(const GemvArgs& a) {
 }
 
 template <int NSTEP, bool GATE>
-void launch_n(GemvArgs a0, GemvArgs a1, bool two, hipStream_t s) {
+void launch_n(GemvArgs a0, GemvArgs a1, bool two, bool nt, hipStream_t s) {
   a0.rows_per_wg = batch_rows(a0);
   const int nb0 = ceil_div(a0.rows, a0.rows_per_wg);
   int grid = nb0;
@@ -214,49 +219,50 @@ void launch_n(GemvArgs a0, GemvArgs a1, bool two, hipStream_t s) {
   } else {
     a1 = a0;
   }
-  CK_LAUNCH((gemv_kernel<NSTEP, GATE>), dim3(grid), dim3(GEMV_THREADS), 0, s, a0, a1, nb0);
+  if (nt) CK_LAUNCH((gemv_kernel<NSTEP, GATE, true>), dim3(grid), dim3(GEMV_THREADS), 0, s, a0, a1, nb0);
+  else CK_LAUNCH((gemv_kernel<NSTEP, GATE, false>), dim3(grid), dim3(GEMV_THREADS), 0, s, a0, a1, nb0);
   CK_LAUNCHED("gemv");
 }
 
 template <bool GATE>
-void launch_args(const GemvArgs& a0, const GemvArgs& a1, bool two, hipStream_t s) {
+void launch_args(const GemvArgs& a0, const GemvArgs& a1, bool two, bool nt, hipStream_t s) {
   const int nstep = ceil_div(two ? std::max(a0.K, a1.K) : a0.K, GEMV_STEP_COLS);
   switch (nstep) {
-    case 1: launch_n<1, GATE>(a0, a1, two, s); break;
-    case 2: launch_n<2, GATE>(a0, a1, two, s); break;
-    case 3: launch_n<3, GATE>(a0, a1, two, s); break;
-    case 4: launch_n<4, GATE>(a0, a1, two, s); break;
-    case 5: launch_n<5, GATE>(a0, a1, two, s); break;
-    case 6: launch_n<6, GATE>(a0, a1, two, s); break;
-    case 7: launch_n<7, GATE>(a0, a1, two, s); break;
-    default: launch_n<8, GATE>(a0, a1, two, s); break;
+    case 1: launch_n<1, GATE>(a0, a1, two, nt, s); break;
+    case 2: launch_n<2, GATE>(a0, a1, two, nt, s); break;
+    case 3: launch_n<3, GATE>(a0, a1, two, nt, s); break;
+    case 4: launch_n<4, GATE>(a0, a1, two, nt, s); break;
+    case 5: launch_n<5, GATE>(a0, a1, two, nt, s); break;
+    case 6: launch_n<6, GATE>(a0, a1, two, nt, s); break;
+    case 7: launch_n<7, GATE>(a0, a1, two, nt, s); break;
+    default: launch_n<8, GATE>(a0, a1, two, nt, s); break;
   }
 }
 
 }  // namespace
 
 void launch_gemv(const half_t* W, const float* x, const float* bias, float* y, int rows, int K, int ldw, int act,
-                 int rows_per_wg, hipStream_t s) {
+                 int rows_per_wg, hipStream_t s, bool stream) {
   const GemvArgs a = make_args(W, x, bias, y, rows, K, ldw, act, rows_per_wg);
   check_args(a);
-  launch_args<false>(a, a, false, s);
+  launch_args<false>(a, a, false, stream, s);
 }
 
 void launch_gemv2(const half_t* W0, const float* x0, const float* b0, float* y0, int rows0, int K0, const half_t* W1,
-                  const float* x1, const float* b1, float* y1, int rows1, int K1, hipStream_t s) {
+                  const float* x1, const float* b1, float* y1, int rows1, int K1, hipStream_t s, bool stream) {
   const GemvArgs a0 = make_args(W0, x0, b0, y0, rows0, K0, K0, GEMV_NONE, 0);
   const GemvArgs a1 = make_args(W1, x1, b1, y1, rows1, K1, K1, GEMV_NONE, 0);
   check_args(a0);
   check_args(a1);
-  launch_args<false>(a0, a1, true, s);
+  launch_args<false>(a0, a1, true, stream, s);
 }
 
 void launch_gemv_gru(const half_t* W, const float* bias, float* y, int rows, const float* gi, const float* gh,
-                     const float* h_prev, float* h_out, float* h_out2, int H, hipStream_t s) {
+                     const float* h_prev, float* h_out, float* h_out2, int H, hipStream_t s, bool stream) {
   GemvArgs a = make_args(W, nullptr, bias, y, rows, H, H, GEMV_NONE, 0);
   a.gi = gi; a.gh = gh; a.hp = h_prev; a.h1 = h_out; a.h2 = h_out2;
   check_args(a);
-  launch_args<true>(a, a, false, s);
+  launch_args<true>(a, a, false, stream, s);
 }
 
 }  // namespace ck

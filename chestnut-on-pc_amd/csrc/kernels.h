@@ -12,16 +12,18 @@ namespace ck {
 // W f16 row-major, x f32, y f32.  K % 8 == 0, ldw % 8 == 0, K <= 16384,
 // W and x 16-byte aligned.  act: 0 none, 1 gelu(tanh).  rows_per_wg: 0 = auto.
 enum GemvAct { GEMV_NONE = 0, GEMV_GELU = 1 };
+// stream: load W non-temporal (the weights pass once; for a model whose
+// weights fit the Infinity Cache the default policy keeps them there).
 void launch_gemv(const half_t* W, const float* x, const float* bias, float* y, int rows, int K,
-                 int ldw, int act, int rows_per_wg, hipStream_t s);
+                 int ldw, int act, int rows_per_wg, hipStream_t s, bool stream = true);
 // Two independent GEMVs (ldw = K, no activation) in one launch.
 void launch_gemv2(const half_t* W0, const float* x0, const float* b0, float* y0, int rows0, int K0, const half_t* W1,
-                  const float* x1, const float* b1, float* y1, int rows1, int K1, hipStream_t s);
+                  const float* x1, const float* b1, float* y1, int rows1, int K1, hipStream_t s, bool stream = true);
 // y = W . h + bias with h the GRU update of gi, gh (gates r, z, n; biases
 // included) and h_prev, computed inside the GEMV; h is also stored to h_out
 // (and h_out2 when non-null).  W is [rows][H].
 void launch_gemv_gru(const half_t* W, const float* bias, float* y, int rows, const float* gi, const float* gh,
-                     const float* h_prev, float* h_out, float* h_out2, int H, hipStream_t s);
+                     const float* h_prev, float* h_out, float* h_out2, int H, hipStream_t s, bool stream = true);
 
 // ---- MFMA GEMM (WMMA attention/projection GEMM analogue) -------------------
 enum Epi {
