@@ -394,8 +394,8 @@ __device__ __forceinline__ void store_staged(const GemmParams& p, const float16_
     constexpr int CPR = WN / 4;   // 16-byte chunks per row
     float* dst = to_ws ? p.ws + ((long)sp * p.batch + bz) * (long)p.M * p.N : static_cast<float*>(p.C) + bz * p.sC;
     const long ld = to_ws ? p.N : p.ldc;
-    const long plane = to_ws ? 4L * p.M * p.N : 0;   // the partials' plane, stored with sc1
-    const bool sc1 = to_ws && sc1_ok(plane);
+    const long plane = to_ws ? 4L * p.M * p.N : 4L * ((long)(p.M - 1) * p.ldc + p.N);
+    const bool sc1 = sc1_ok(plane);
     const __amdgpu_buffer_rsrc_t rs = sc1_rsrc(dst, sc1 ? plane : 0);
 #pragma unroll 4
     for (int q = lane; q < WM * CPR; q += 64) {

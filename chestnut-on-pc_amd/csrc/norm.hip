@@ -153,7 +153,8 @@ __global__ __launch_bounds__(256) void layernorm_row_kernel(float* __restrict__ 
       if constexpr (VW == 4) store_sc1(sc1_rsrc(static_cast<half_t*>(out) + (long)row * D, 2L * D), 2L * (c - (long)row * D), h);
       else *reinterpret_cast<hvec_t*>(static_cast<half_t*>(out) + c) = h;
     } else {
-      *reinterpret_cast<vec_t*>(static_cast<float*>(out) + c) = y;
+      if constexpr (VW == 4) store_sc1(sc1_rsrc(static_cast<float*>(out) + (long)row * D, 4L * D), 4L * (c - (long)row * D), y);
+      else *reinterpret_cast<vec_t*>(static_cast<float*>(out) + c) = y;
     }
   }
 }

@@ -58,10 +58,12 @@ __global__ __launch_bounds__(256) void policy_inputs_kernel(const PolicyArgs a) 
     const int new_slot = wrap(n, a.img_slots);
     uint8_t* ring = a.img_ring + (long)s * a.img_slots * fb;
     const u32x4_t old = reinterpret_cast<const u32x4_t*>(ring + old_slot * fb)[u];
-    uint8_t* out = a.img_out + (long)s * 2 * fb;
-    reinterpret_cast<u32x4_t*>(out)[u] = old;
-    reinterpret_cast<u32x4_t*>(out + fb)[u] = cur;
-    reinterpret_cast<u32x4_t*>(ring + new_slot * fb)[u] = cur;
+    // device-scope stores (store_sc1): the conv stem reads these next
+    const __amdgpu_buffer_rsrc_t ro = sc1_rsrc(a.img_out, 4L * fb);
+    const __amdgpu_buffer_rsrc_t rr = sc1_rsrc(a.img_ring, 2L * a.img_slots * fb);
+    store_sc1(ro, (long)s * 2 * fb + 16L * u, __builtin_bit_cast(float4_t, old));
+    store_sc1(ro, (long)s * 2 * fb + fb + 16L * u, __builtin_bit_cast(float4_t, cur));
+    store_sc1(rr, ((long)s * a.img_slots + new_slot) * fb + 16L * u, __builtin_bit_cast(float4_t, cur));
     return;
   }
   i -= a.n_img;
@@ -204,7 +206,7 @@ __global__ __launch_bounds__(256) void im2col_u8_kernel(const uint8_t* __restric
       ++tap;
     }
   }
-  *reinterpret_cast<half8_t*>(patches + ((long)b * Ho * Wo + p) * Kp + k0) = v;
+  store_sc1(sc1_rsrc(patches, 2L * gridDim.y * Ho * Wo * Kp), 2L * (((long)b * Ho * Wo + p) * Kp + k0), v);
 }
 
 // Later layers: f16 activations [batch][H][W][C] = an image of A=H rows of
