@@ -600,8 +600,10 @@ void ck_engine::build_plan() {
   // follows each of them adds partials + bias into x before normalising.
   // Tiles and splits were chosen on whole frames of the 1B model (a GEMM's
   // time inside the frame differs from its time in a loop of its own):
-  //   QKV, MLP up: 128x128, one K-group;  O-proj: 128x64 split to fill 256
-  //   workgroups;  MLP down: 128x128, one K-group, split to fill 256.
+  //   QKV, MLP up: 128x128, one K-group;  O-proj: 64x128, two K-groups,
+  //   split to fill 256 workgroups (128x64 until the cache-policy changes of
+  //   the stores and weight loads; retuned: -1.5% of the 1B frame);  MLP
+  //   down: 128x128, one K-group, split to fill 256.
   //   GEMMs whose 128x128 tiles would leave most CUs idle (fewer than 64
   //   tiles: the 39M model's 256 tokens x d = 512) run on 64x64 tiles with
   //   one K-group, the residual ones split down to 4 K-steps per workgroup
@@ -613,9 +615,9 @@ void ck_engine::build_plan() {
     while (tiles * s * 2 <= 256 && K % (kmult * s * 2) == 0 && K / (s * 2) >= kmin) s *= 2;
     return s;
   };
-  const int tile_o = small(d) ? 8 : 2, tile_dn = small(d) ? 8 : 5;
+  const int tile_o = small(d) ? 8 : 3, tile_dn = small(d) ? 8 : 5;
   const int tile_qkv = small(3 * d) ? 8 : 5, tile_up = small(F) ? 8 : 5;
-  const int s_o = small(d) ? resid_split(T, d, d, 64, 64, 64, 256) : resid_split(T, d, d, 128, 64, 128, 512);
+  const int s_o = small(d) ? resid_split(T, d, d, 64, 64, 64, 256) : resid_split(T, d, d, 64, 128, 128, 512);
   const int s_dn = small(d) ? resid_split(T, d, F, 64, 64, 64, 256) : resid_split(T, d, F, 128, 128, 128, 512);
   ck_engine* self = this;
   const long part_stride = (long)T * d;
@@ -655,7 +657,7 @@ void ck_engine::build_plan() {
     });
     GemmDesc o;
     o.A = att; o.lda = d; o.B = h16(p + "o.w"); o.ldb = d;
-    o.M = T; o.N = d; o.K = d; o.epi = EPI_PARTIALS; o.tile = tile_o; o.split = s_o;   // 128x64 (64x64 when small)
+    o.M = T; o.N = d; o.K = d; o.epi = EPI_PARTIALS; o.tile = tile_o; o.split = s_o;   // 64x128 (64x64 when small)
     pend_split = add_gemm(b + "o", "gemm_partials", o);   // the split actually used (gemm_config may set it)
     pend_bias = f32(p + "o.b");
     add_ln(b + "ln2", f32(p + "ln2.g"), f32(p + "ln2.b"), hb, true);
