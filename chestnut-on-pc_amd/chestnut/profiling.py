@@ -254,7 +254,9 @@ def configs_md(res, cmd):
            'Commands (run from the repository root on the MI355X box; the counter passes each a run of their own):',
            '', '```', cmd, '```', '',
            f"Timed: {run['units_timed']} {run['unit']}s over rotating operand copies (more than the 256 MB Infinity "
-           f"Cache), after one untimed pass.  Kernel trace: {unit_us:.2f} us per {run['unit']} (the sum of the "
+           f"Cache), after one untimed pass" + (f" and {run['warmup_ms']:.0f} ms of untimed repetitions (the "
+           "GPU's clocks ramp up over the first tens of milliseconds of sustained load)"
+           if run.get('warmup_ms') else '') + f".  Kernel trace: {unit_us:.2f} us per {run['unit']} (the sum of the "
            f"per-kernel medians).  Algorithmic work per {run['unit']}: {run['flops'] / 1e9:.3f} GFLOP, "
            f"{run['bytes'] / 1e6:.2f} MB; roofline floor t_min = max(flops / 2.5 PFLOP/s, bytes / 8 TB/s) = "
            f"{t_min:.2f} us, so the {run['unit']} runs at {t_min / unit_us:.3f} of its roofline.  (The HIP-event "
