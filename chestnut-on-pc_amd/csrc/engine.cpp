@@ -94,6 +94,7 @@ Spec parse_spec(const std::string& json) {
                "spec: camera needs an even width and height, stride >= width, y_height >= height");
   }
   s.overlap = jint(o, "overlap_context", -1);
+  s.fuse_temporal = jint(o, "fuse_temporal", -1);
   if (const JVal* gc = o.get("gemm_config")) {
     CK_REQUIRE(gc->kind == JVal::OBJ, "spec: gemm_config must be an object {entry: [tile, split]}");
     for (const auto& kv : gc->obj) {
@@ -483,16 +484,32 @@ void ck_engine::build_plan() {
   // `overlap` they run on a second stream forked after the inputs, beside
   // the conv stem, and the embedding waits for them.
   const bool overlap = sp.overlap >= 0 ? sp.overlap != 0 : false;
+  // Without the second stream the temporal GEMV shares the launch of stem
+  // layer 1's im2col (both wait only on the inputs) when its workgroups leave
+  // resident slots free: one dependent dispatch fewer, and the im2col runs in
+  // those slots beside the GEMV (39M frame -0.7%: the pair takes 11.9 us
+  // against 6.6 + 8.6).  The 1B model's GEMV alone fills every slot (768
+  // workgroups) and the shared launch leaves its frame unchanged within noise.
+  const int Kt = sp.feat_hist * sp.feat_len, Td = sp.temporal_dim;
+  bool fuse_tmp = !overlap && sp.fuse_temporal != 0;
+  int tmp_slots = 0;
+  if (fuse_tmp) {
+    tmp_slots = gemv_im2col_u8_slots(Kt, stream_w);   // a device query: here, never under graph capture
+    if (sp.fuse_temporal < 0) fuse_tmp = gemv_workgroups(Td) < tmp_slots;
+  }
+  const double tmp_flops = 2.0 * Td * Kt, tmp_bytes = (double)Td * Kt * 2 + Kt * 4 + Td * 8;
   auto add_context = [&](int branch) {
-    const int Kt = sp.feat_hist * sp.feat_len, Td = sp.temporal_dim;
-    const half_t* tw = h16("tmp.w");
-    const float* tb = f32("tmp.b");
-    const float* fbuf = f32("feat_buf");
+    if (!fuse_tmp) {
+      const half_t* tw = h16("tmp.w");
+      const float* tb = f32("tmp.b");
+      const float* fbuf = f32("feat_buf");
+      float* cin = f32("ctx_in");
+      add("temporal", "gemv", tmp_flops, tmp_bytes, [=](hipStream_t s) {
+        launch_gemv(tw, fbuf, tb, cin, Td, Kt, Kt, GEMV_GELU, 0, s, stream_w);
+      });
+      plan.back().branch = branch;
+    }
     float* cin = f32("ctx_in");
-    add("temporal", "gemv", 2.0 * Td * Kt, (double)Td * Kt * 2 + Kt * 4 + Td * 8, [=](hipStream_t s) {
-      launch_gemv(tw, fbuf, tb, cin, Td, Kt, Kt, GEMV_GELU, 0, s, stream_w);
-    });
-    plan.back().branch = branch;
     const half_t* cw = h16("ctx.w");
     const float* cb = f32("ctx.b");
     float* ctx = f32("ctx");
@@ -553,9 +570,21 @@ void ck_engine::build_plan() {
       }
       if (i == 0) {
         const uint8_t* img = static_cast<uint8_t*>(ptr("img"));
-        add("stem0.im2col", "im2col_u8", 0, pbytes + 2.0 * C * HW, [=](hipStream_t s) {
-          launch_im2col_u8(img, 2, C, H, W, patches, Kp, s);
-        });
+        if (fuse_tmp) {
+          const half_t* tw = h16("tmp.w");
+          const float* tb = f32("tmp.b");
+          const float* fbuf = f32("feat_buf");
+          float* cin = f32("ctx_in");
+          const int slots = tmp_slots;
+          add("stem0.im2col", "gemv_im2col_u8", tmp_flops, tmp_bytes + pbytes + 2.0 * C * HW, [=](hipStream_t s) {
+            launch_gemv_im2col_u8(tw, fbuf, tb, cin, Td, Kt, GEMV_GELU, stream_w, img, 2, C, H, W, patches, Kp, slots,
+                                  s);
+          });
+        } else {
+          add("stem0.im2col", "im2col_u8", 0, pbytes + 2.0 * C * HW, [=](hipStream_t s) {
+            launch_im2col_u8(img, 2, C, H, W, patches, Kp, s);
+          });
+        }
       } else {
         const half_t* prev = h16("stem." + std::to_string(i - 1) + ".out");
         add("stem" + si + ".im2col", "im2col_f16", 0, pbytes + 2.0 * H * W * C * 2, [=](hipStream_t s) {

@@ -31,6 +31,7 @@
 #include <algorithm>
 
 #include "common.h"
+#include "im2col_u8.h"
 #include "kernels.h"
 
 namespace ck {
@@ -59,13 +60,15 @@ struct GemvArgs {
   float* h2;
 };
 
+// Workgroup `bid` of a GEMV launch (the body of gemv_kernel, also run by the
+// GEMV workgroups of gemv_im2col_kernel).
 template <int NSTEP, bool GATE, bool NT>
-__global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(const GemvArgs a0, const GemvArgs a1, int nb0) {
+__device__ __forceinline__ void gemv_block(const GemvArgs& a0, const GemvArgs& a1, int nb0, int bid) {
   __shared__ float red[2][4][GEMV_RB];
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  const bool second = (int)blockIdx.x >= nb0;
+  const bool second = bid >= nb0;
   const GemvArgs& a = second ? a1 : a0;
-  const int blk = second ? (int)blockIdx.x - nb0 : (int)blockIdx.x;
+  const int blk = second ? bid - nb0 : bid;
   const half_t* __restrict__ W = a.W;
   const int rows = a.rows, K = a.K, ldw = a.ldw;
 
@@ -179,6 +182,57 @@ __global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(const GemvArgs a0, c
   }
 }
 
+template <int NSTEP, bool GATE, bool NT>
+__global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(const GemvArgs a0, const GemvArgs a1, int nb0) {
+  gemv_block<NSTEP, GATE, NT>(a0, a1, nb0, (int)blockIdx.x);
+}
+
+// Layer-1 im2col of the conv stem (im2col_u8_gather) for `batch` images,
+// `blocks_per_image` 256-thread blocks each.  In the shared launch its
+// blocks are folded onto `nblk` workgroups, U blocks per workgroup.
+struct Im2colU8Args {
+  const uint8_t* img;
+  half_t* patches;
+  int C, H, W, Kp, Ho, Wo, batch, blocks_per_image, nblk;
+};
+
+// One launch for two independent pieces of work that each leave part of the
+// chip idle: workgroups [0, nb) run the GEMV `a`, the next `nblk` the
+// im2col.  The GEMV's workgroups come first so its weight stream starts at
+// once; the im2col's take the slots the GEMV leaves free (the host sizes
+// nblk to them), each running U of the im2col's blocks with every gather
+// load issued before the first store, so the whole im2col is resident in one
+// round beside the GEMV (the temporal GEMV and stem layer 1 both wait only on
+// the policy inputs).
+template <int NSTEP, bool NT, int U>
+__global__ __launch_bounds__(GEMV_THREADS) void gemv_im2col_kernel(const GemvArgs a, int nb, const Im2colU8Args c) {
+  const int bid = (int)blockIdx.x;
+  if (bid < nb) {
+    gemv_block<NSTEP, false, NT>(a, a, nb, bid);
+    return;
+  }
+  const int total = c.batch * c.blocks_per_image;
+  half8_t v[U];
+  long off[U];
+  bool ok[U];
+  const int per = c.Ho * c.Wo * (c.Kp / 8);
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    // clamped to the last valid block and item (their stores are dropped),
+    // so no gather sits under a branch and all U gathers issue together
+    const int j0 = bid - nb + u * c.nblk, j = min(j0, total - 1);
+    const int b = j / c.blocks_per_image;
+    const int i0 = (j - b * c.blocks_per_image) * GEMV_THREADS + (int)threadIdx.x, i = min(i0, per - 1);
+    im2col_u8_gather(c.img, c.C, c.H, c.W, c.Kp, c.Ho, c.Wo, b, i, v[u], off[u]);
+    ok[u] = j0 < total && i0 < per;
+  }
+  // device-scope stores: the layer-1 conv GEMM reads the patches next
+  const auto rsrc = sc1_rsrc(c.patches, 2L * c.batch * c.Ho * c.Wo * c.Kp);
+#pragma unroll
+  for (int u = 0; u < U; ++u)
+    if (ok[u]) store_sc1(rsrc, off[u], v[u]);
+}
+
 GemvArgs make_args(const half_t* W, const float* x, const float* bias, float* y, int rows, int K, int ldw, int act,
                    int rows_per_wg) {
   GemvArgs a{};
@@ -239,7 +293,100 @@ void launch_args(const GemvArgs& a0, const GemvArgs& a1, bool two, bool nt, hipS
   }
 }
 
+// Resident workgroups of the shared launch over the whole current device.
+template <int NSTEP, bool NT>
+int resident_slots() {
+  int dev = 0, per_cu = 0, cus = 0;
+  CK_HIP(hipGetDevice(&dev));
+  CK_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+  CK_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(
+      &per_cu, reinterpret_cast<const void*>(gemv_im2col_kernel<NSTEP, NT, 1>), GEMV_THREADS, 0));
+  return std::max(1, per_cu) * std::max(1, cus);
+}
+
+template <int NSTEP, bool NT, int U>
+void launch_fused_u(const GemvArgs& a, int nb, const Im2colU8Args& c, hipStream_t s) {
+  CK_LAUNCH((gemv_im2col_kernel<NSTEP, NT, U>), dim3((unsigned)(nb + c.nblk)), dim3(GEMV_THREADS), 0, s, a, nb, c);
+}
+
+template <int NSTEP, bool NT>
+void launch_fused(GemvArgs a, Im2colU8Args c, int slots, hipStream_t s) {
+  a.rows_per_wg = batch_rows(a);
+  const int nb = ceil_div(a.rows, a.rows_per_wg);
+  const long total = (long)c.batch * c.blocks_per_image;
+  CK_REQUIRE(total < (1L << 30), "gemv_im2col_u8: image too large");
+  // the slots the GEMV leaves free, at least a quarter of the im2col's blocks
+  const long free_slots = std::max<long>((long)slots - nb, ceil_div(total, 4));
+  const int u = (int)std::min<long>(4, ceil_div(total, free_slots));
+  const int U = u <= 1 ? 1 : u == 2 ? 2 : 4;
+  c.nblk = ceil_div(total, U);
+  if (U == 1) launch_fused_u<NSTEP, NT, 1>(a, nb, c, s);
+  else if (U == 2) launch_fused_u<NSTEP, NT, 2>(a, nb, c, s);
+  else launch_fused_u<NSTEP, NT, 4>(a, nb, c, s);
+  CK_LAUNCHED("gemv_im2col_u8");
+}
+
+template <int NSTEP>
+void launch_fused_nt(const GemvArgs& a, const Im2colU8Args& c, bool nt, int slots, hipStream_t s) {
+  if (slots <= 0) slots = nt ? resident_slots<NSTEP, true>() : resident_slots<NSTEP, false>();
+  if (nt) launch_fused<NSTEP, true>(a, c, slots, s);
+  else launch_fused<NSTEP, false>(a, c, slots, s);
+}
+
+template <int NSTEP>
+int slots_nt(bool nt) {
+  return nt ? resident_slots<NSTEP, true>() : resident_slots<NSTEP, false>();
+}
+
 }  // namespace
+
+int gemv_workgroups(int rows) {
+  CK_REQUIRE(rows > 0, "gemv: rows must be positive");
+  GemvArgs a{};
+  a.rows = rows;
+  return ceil_div(rows, batch_rows(a));
+}
+
+int gemv_im2col_u8_slots(int K, bool stream) {
+  CK_REQUIRE(K > 0 && K <= 8 * GEMV_STEP_COLS, "gemv_im2col_u8: K must be in (0, 16384]");
+  switch (ceil_div(K, GEMV_STEP_COLS)) {
+    case 1: return slots_nt<1>(stream);
+    case 2: return slots_nt<2>(stream);
+    case 3: return slots_nt<3>(stream);
+    case 4: return slots_nt<4>(stream);
+    case 5: return slots_nt<5>(stream);
+    case 6: return slots_nt<6>(stream);
+    case 7: return slots_nt<7>(stream);
+    default: return slots_nt<8>(stream);
+  }
+}
+
+void launch_gemv_im2col_u8(const half_t* Wt, const float* x, const float* bias, float* y, int rows, int K, int act,
+                           bool stream, const uint8_t* img, int batch, int C, int H, int W, half_t* patches, int Kp,
+                           int slots, hipStream_t s) {
+  const GemvArgs a = make_args(Wt, x, bias, y, rows, K, K, act, 0);
+  check_args(a);
+  CK_REQUIRE(img && patches && batch > 0 && C > 0 && H > 0 && W > 0, "gemv_im2col_u8: bad im2col arguments");
+  CK_REQUIRE(Kp >= 9 * C && Kp % 8 == 0, "gemv_im2col_u8: Kp must be >= 9C and a multiple of 8");
+  CK_REQUIRE((reinterpret_cast<uintptr_t>(patches) & 15) == 0, "gemv_im2col_u8: patches must be 16-byte aligned");
+  Im2colU8Args c{};
+  c.img = img; c.patches = patches; c.C = C; c.H = H; c.W = W; c.Kp = Kp; c.batch = batch;
+  c.Ho = (H - 1) / 2 + 1;
+  c.Wo = (W - 1) / 2 + 1;
+  const long per = (long)c.Ho * c.Wo * (Kp / 8);
+  CK_REQUIRE(per < (1L << 31) && (long)H * W < (1L << 31), "gemv_im2col_u8: image too large");
+  c.blocks_per_image = (int)ceil_div(per, GEMV_THREADS);
+  switch (ceil_div(K, GEMV_STEP_COLS)) {
+    case 1: launch_fused_nt<1>(a, c, stream, slots, s); break;
+    case 2: launch_fused_nt<2>(a, c, stream, slots, s); break;
+    case 3: launch_fused_nt<3>(a, c, stream, slots, s); break;
+    case 4: launch_fused_nt<4>(a, c, stream, slots, s); break;
+    case 5: launch_fused_nt<5>(a, c, stream, slots, s); break;
+    case 6: launch_fused_nt<6>(a, c, stream, slots, s); break;
+    case 7: launch_fused_nt<7>(a, c, stream, slots, s); break;
+    default: launch_fused_nt<8>(a, c, stream, slots, s); break;
+  }
+}
 
 void launch_gemv(const half_t* W, const float* x, const float* bias, float* y, int rows, int K, int ldw, int act,
                  int rows_per_wg, hipStream_t s, bool stream) {

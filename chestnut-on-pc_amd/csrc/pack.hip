@@ -1,6 +1,7 @@
 // Integer-exact input-side kernels: policy input queues, uint8 frame packing,
 // image2d zero-border gathers and the conv-stem im2col built on them.
 #include "common.h"
+#include "im2col_u8.h"
 #include "kernels.h"
 
 namespace ck {
@@ -172,41 +173,11 @@ void gather_launch(const void* img, int A, int B, const int* yx, int n, void* ou
 // column k = (ky*3 + kx)*C + c, zero-padded to Kp columns.  Every input read
 // is an image2d texel read with a zero border.
 // ---------------------------------------------------------------------------
-// Layer 1: uint8 planes [batch][C][H][W], each plane an image of A=H rows of
-// B=W one-byte texels; value (u8 - 128) / 128, zero outside the image.
-// Thread per 8 consecutive columns of a patch row: one 16-byte store, and the
-// (tap, channel) pair of each column advanced by increment instead of a
-// division per element (32-bit index math; the host checks the sizes fit).
+// Layer 1: uint8 planes [batch][C][H][W] (im2col_u8_at, im2col_u8.h).
 __global__ __launch_bounds__(256) void im2col_u8_kernel(const uint8_t* __restrict__ img, int C, int H, int W,
                                                         half_t* __restrict__ patches, int Kp, int Ho, int Wo) {
-  const int i = blockIdx.x * 256 + threadIdx.x;
-  const int kg = Kp / 8;
-  const int per = Ho * Wo * kg;
-  const int b = blockIdx.y;
-  if (i >= per) return;
-  const int p = i / kg, k0 = (i - p * kg) * 8;
-  const int ho = p / Wo, wo = p - ho * Wo;
-  int tap = k0 / C, c = k0 - tap * C;
-  const uint8_t* base = img + (long)b * C * H * W;
-  half8_t v;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    float f = 0.f;
-    if (tap < 9) {
-      const int y = 2 * ho - 1 + tap / 3, x = 2 * wo - 1 + tap % 3;
-      const int fl = y * W + x;
-      const int fc = min(max(fl, 0), H * W - 1);
-      const bool valid = (x >= 0) & (x < W) & (y >= 0) & (y < H);
-      const uint8_t u = base[(long)c * H * W + fc];
-      f = valid ? ((float)u - 128.0f) * 0.0078125f : 0.f;
-    }
-    v[e] = (half_t)f;
-    if (++c == C) {
-      c = 0;
-      ++tap;
-    }
-  }
-  store_sc1(sc1_rsrc(patches, 2L * gridDim.y * Ho * Wo * Kp), 2L * (((long)b * Ho * Wo + p) * Kp + k0), v);
+  im2col_u8_at(img, C, H, W, patches, Kp, Ho, Wo, (int)gridDim.y, (int)blockIdx.y,
+               (int)(blockIdx.x * 256 + threadIdx.x));
 }
 
 // Later layers: f16 activations [batch][H][W][C] = an image of A=H rows of

@@ -407,6 +407,55 @@ def test_overlapped_context_branch_is_bit_identical(tiny, graph):
         np.testing.assert_array_equal(a, b)
 
 
+@pytest.mark.parametrize('spec_name,graph', [('tiny', True), ('tiny', False), ('driving_39m', True),
+                                             ('big_driving_1b', True)])
+def test_temporal_gemv_fused_with_stem_im2col_is_bit_identical(gpu, spec_name, graph):
+    """The temporal GEMV carried in stem layer 1's im2col launch (its
+    workgroups first, the im2col's folded onto the slots it leaves free: one,
+    two or four im2col blocks per workgroup across these specs) gives the same
+    bits as the two separate launches, frame after frame; with the side
+    stream on, the option is ignored and the temporal GEMV keeps its own
+    entry."""
+    sp = S.get_spec(spec_name)
+    w = S.make_weights(sp)
+    rng = np.random.default_rng(16)
+    frames = list(frame_inputs(rng, spec_name, 3))
+    outs = []
+    for fuse in (0, 1):
+        with Engine(dict(sp, fuse_temporal=fuse, overlap_context=0), weights=w, graph=graph) as e:
+            plan = {p['name']: p['kernel'] for p in e.plan()}
+            assert ('temporal' in plan) == (not fuse)
+            assert plan['stem0.im2col'] == ('gemv_im2col_u8' if fuse else 'im2col_u8')
+            res, hs = [], None
+            for warped, packed in frames:
+                packed = packed.copy()
+                if hs is not None:
+                    packed[12:] = hs
+                o = e.run_frame(warped, packed)
+                hs = o[e.out_slices['hidden_state']]
+                res.append(o)
+            outs.append(res)
+    print(f'[fuse] {spec_name} graph={graph}: {len(frames)} frames compared', flush=True)
+    for a, b in zip(*outs):
+        np.testing.assert_array_equal(a, b)
+    if spec_name == 'tiny':
+        with Engine(dict(sp, fuse_temporal=1, overlap_context=1), weights=w, graph=graph) as e:
+            plan = {p['name']: p['kernel'] for p in e.plan()}
+            assert plan['temporal'] == 'gemv' and plan['stem0.im2col'] == 'im2col_u8'
+
+
+def test_temporal_fusion_default_follows_free_slots(gpu):
+    """By default the temporal GEMV shares the im2col launch only when its
+    workgroups leave resident slots free: the 39M model's 1664 rows (416
+    workgroups) do, the 1B model's 3072 (768, every slot at three
+    workgroups per CU) do not."""
+    for name, fused in (('driving_39m', True), ('big_driving_1b', False)):
+        with Engine(S.get_spec(name)) as e:
+            plan = {p['name']: p['kernel'] for p in e.plan()}
+        assert (plan['stem0.im2col'] == 'gemv_im2col_u8') == fused, name
+        assert ('temporal' in plan) == (not fused), name
+
+
 @pytest.mark.parametrize('spec_name', ['tiny', 'driving_39m'])
 def test_stem_layer1_vs_oracle_frame_after_frame(gpu, spec_name):
     """Conv-stem layer 1 (zero-border im2col of the sampled 12-channel image +
