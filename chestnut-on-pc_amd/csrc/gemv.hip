@@ -200,7 +200,7 @@ struct Im2colU8Args {
 // chip idle: workgroups [0, nb) run the GEMV `a`, the next `nblk` the
 // im2col.  The GEMV's workgroups come first so its weight stream starts at
 // once; the im2col's take the slots the GEMV leaves free (the host sizes
-// nblk to them), each running U of the im2col's blocks with every gather
+// nblk to them), each running U (1-4) of the im2col's blocks with every gather
 // load issued before the first store, so the whole im2col is resident in one
 // round beside the GEMV (the temporal GEMV and stem layer 1 both wait only on
 // the policy inputs).
@@ -317,11 +317,11 @@ void launch_fused(GemvArgs a, Im2colU8Args c, int slots, hipStream_t s) {
   CK_REQUIRE(total < (1L << 30), "gemv_im2col_u8: image too large");
   // the slots the GEMV leaves free, at least a quarter of the im2col's blocks
   const long free_slots = std::max<long>((long)slots - nb, ceil_div(total, 4));
-  const int u = (int)std::min<long>(4, ceil_div(total, free_slots));
-  const int U = u <= 1 ? 1 : u == 2 ? 2 : 4;
+  const int U = (int)std::min<long>(4, ceil_div(total, free_slots));
   c.nblk = ceil_div(total, U);
   if (U == 1) launch_fused_u<NSTEP, NT, 1>(a, nb, c, s);
   else if (U == 2) launch_fused_u<NSTEP, NT, 2>(a, nb, c, s);
+  else if (U == 3) launch_fused_u<NSTEP, NT, 3>(a, nb, c, s);
   else launch_fused_u<NSTEP, NT, 4>(a, nb, c, s);
   CK_LAUNCHED("gemv_im2col_u8");
 }

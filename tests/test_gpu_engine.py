@@ -411,15 +411,15 @@ def test_overlapped_context_branch_is_bit_identical(tiny, graph):
                                              ('big_driving_1b', True)])
 def test_temporal_gemv_fused_with_stem_im2col_is_bit_identical(gpu, spec_name, graph):
     """The temporal GEMV carried in stem layer 1's im2col launch (its
-    workgroups first, the im2col's folded onto the slots it leaves free: one,
-    two or four im2col blocks per workgroup across these specs) gives the same
-    bits as the two separate launches, frame after frame; with the side
-    stream on, the option is ignored and the temporal GEMV keeps its own
-    entry."""
+    workgroups first, the im2col's 1024 blocks folded onto the slots it
+    leaves free: at three resident workgroups per CU, 2 blocks per workgroup
+    for tiny, 3 for 39M, 4 for 1B) gives the same bits as the two separate
+    launches, frame after frame; with the side stream on, the option is
+    ignored and the temporal GEMV keeps its own entry."""
     sp = S.get_spec(spec_name)
     w = S.make_weights(sp)
     rng = np.random.default_rng(16)
-    frames = list(frame_inputs(rng, spec_name, 3))
+    frames = list(frame_inputs(rng, sp, 3))
     outs = []
     for fuse in (0, 1):
         with Engine(dict(sp, fuse_temporal=fuse, overlap_context=0), weights=w, graph=graph) as e:
