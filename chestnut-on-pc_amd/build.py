@@ -58,9 +58,31 @@ def build(jobs=8, verbose=False):
     return LIB
 
 
+VENDOR = os.path.join(HERE, 'vendor_compare')
+
+
+def build_vendor_compare():
+    """The config-1 comparison against hipBLASLt (vendor_compare/), linked
+    against the built library; run it from anywhere."""
+    src = os.path.join(VENDOR, 'config1_hipblaslt.cpp')
+    exe = os.path.join(VENDOR, 'config1_hipblaslt')
+    inc = os.path.join(os.path.dirname(HERE), 'include')
+    libdir = os.path.dirname(LIB)
+    cmd = [HIPCC] + COMMON + DEVICE_ONLY + ['-I', inc, src, '-o', exe, '-L', libdir, '-lchestnut', '-lhipblaslt',
+                                            f'-Wl,-rpath,{libdir}', "-Wl,-rpath,$ORIGIN/../chestnut"]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError('vendor comparison build failed:\n' + r.stdout + r.stderr)
+    return exe
+
+
 if __name__ == '__main__':
     ap = argparse.ArgumentParser()
     ap.add_argument('-j', type=int, default=8)
     ap.add_argument('-v', action='store_true')
+    ap.add_argument('--vendor-compare', action='store_true',
+                    help='also build vendor_compare/config1_hipblaslt (needs the library built first)')
     a = ap.parse_args()
     print(build(a.j, a.v))
+    if a.vendor_compare:
+        print(build_vendor_compare())
