@@ -893,10 +893,12 @@ void launch_epi_cv(int tile, const GemmParams& p, hipStream_t s) {
   }
 }
 
-// 128x128 LDS-DMA tile for a [K][N] B (f32 output), two K-groups (tile 1) or one.
-void launch_dma_bt(const GemmParams& p, bool kg2, hipStream_t s) {
+// LDS-DMA tiles for a [K][N] B (f32 output): 128x128 with two K-groups (tile
+// 1) or one, and 256x128 with 8 waves in one K-group (tile 9, 3-stage ring).
+void launch_dma_bt(const GemmParams& p, int tile, bool kg2, hipStream_t s) {
   const int grid = p.Mt * p.Nt * p.split * p.batch;
-  if (kg2) CK_LAUNCH((gemm_dma_kernel<128, 128, 4, 2, EPI_F32, 4, true>), dim3(grid), dim3(512), 0, s, p);
+  if (tile == 9) CK_LAUNCH((gemm_dma_kernel<256, 128, 3, 1, EPI_F32, 8, true>), dim3(grid), dim3(512), 0, s, p);
+  else if (kg2) CK_LAUNCH((gemm_dma_kernel<128, 128, 4, 2, EPI_F32, 4, true>), dim3(grid), dim3(512), 0, s, p);
   else CK_LAUNCH((gemm_dma_kernel<128, 128, 5, 1, EPI_F32, 4, true>), dim3(grid), dim3(256), 0, s, p);
   CK_LAUNCHED("gemm_dma_bt");
 }
@@ -959,7 +961,9 @@ void launch_reduce(const GemmParams& p, hipStream_t s) {
 // it lies and read transposed (no transpose pass, no workspace for it).
 // (A and B are required to be 16-byte aligned for every launch.)
 bool bt_direct(const GemmDesc& d) {
-  return d.b_kn && d.tile == 1 && (d.K / d.split) % (2 * BK) == 0 && d.N % 128 == 0;
+  if (!d.b_kn || d.N % 128 != 0) return false;
+  if (d.tile == 1) return (d.K / d.split) % (2 * BK) == 0;
+  return d.tile == 9;   // 256x128, 8 waves in one K-group
 }
 
 int tile_base(int tile) { const int c = tile % 10; return c > 4 ? c - 4 : c; }
@@ -1099,7 +1103,7 @@ void launch_gemm(GemmDesc d, hipStream_t s) {
     // pass).  Only with two K-groups: on one (tile 5) the doubled fragment
     // reads cost more than the transpose pass saves (config 1: 44.6 against
     // 33.2 us; two K-groups 32.6 against 34.9 us).
-    launch_dma_bt(p, true, s);
+    launch_dma_bt(p, d.tile, true, s);
     if (d.split > 1) launch_reduce<EPI_F32>(p, s);
     return;
   }

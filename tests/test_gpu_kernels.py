@@ -153,15 +153,16 @@ def test_gemm_config1_full_size(gpu):
     _gemm_check(Ct, A, B)
 
 
-@pytest.mark.parametrize('tile', [0, 1, 4, 5, 11, 13])
+@pytest.mark.parametrize('tile', [0, 1, 4, 5, 9, 11, 13])
 @pytest.mark.parametrize('M,N,Kd,split', [(100, 200, 320, 1), (300, 136, 1024, 2), (100, 256, 384, 1),
                                           (300, 384, 1024, 4), (64, 128, 256, 2)])
 def test_gemm_kn_paths(gpu, tile, M, N, Kd, split):
     """[K][N] B: with N a multiple of 128 the two-K-group 128x128 LDS-DMA
-    tile (1, and 0 when it picks it) streams it into LDS as it is and reads
-    its MFMA fragments transposed; otherwise the LDS-DMA tiles (4, 5, ...)
-    transpose it into the workspace first, and the register-staged tiles
-    (11, 13) transpose it in registers; ragged M and N."""
+    tile (1, and 0 when it picks it) and the 8-wave 256x128 tile (9) stream
+    it into LDS as it is and read their MFMA fragments transposed; otherwise
+    the LDS-DMA tiles (4, 5, 9, ...) transpose it into the workspace first,
+    and the register-staged tiles (11, 13) transpose it in registers; ragged
+    M and N."""
     from chestnut import kernels as K
     rng = np.random.default_rng(M + N + tile)
     A = rng.standard_normal((M, Kd)).astype(np.float16)
