@@ -94,7 +94,7 @@ Spec parse_spec(const std::string& json) {
                "spec: camera needs an even width and height, stride >= width, y_height >= height");
   }
   s.overlap = jint(o, "overlap_context", -1);
-  s.fuse_temporal = jint(o, "fuse_temporal", -1);
+  s.fuse_head = jint(o, "fuse_head", 1);
   if (const JVal* gc = o.get("gemm_config")) {
     CK_REQUIRE(gc->kind == JVal::OBJ, "spec: gemm_config must be an object {entry: [tile, split]}");
     for (const auto& kv : gc->obj) {
@@ -462,6 +462,14 @@ void ck_engine::build_plan() {
   auto h16 = [&](const std::string& n) { return static_cast<half_t*>(ptr(n)); };
   auto f32 = [&](const std::string& n) { return static_cast<float*>(ptr(n)); };
 
+  const bool overlap = sp.overlap >= 0 ? sp.overlap != 0 : false;
+  const int Kt = sp.feat_hist * sp.feat_len, Td = sp.temporal_dim;
+  const double tmp_flops = 2.0 * Td * Kt, tmp_bytes = (double)Td * Kt * 2 + Kt * 4 + Td * 8;
+  // The frame head: the policy inputs, the temporal GEMV and stem layer 1's
+  // im2col in one launch (launch_frame_head), none of them waiting on
+  // another: two dependent dispatches fewer (whole frames in alternating
+  // processes: 39M -1.2 to -2.2%, 1B -0.4%; bit-identical).
+  const bool head = !overlap && sp.fuse_head != 0;
   // 1. policy inputs: queue push + sample (compile_modeld.py:198-212)
   {
     QueueDims q{sp.img_h, sp.img_w, sp.fs, sp.fs * (sp.n_frames - 1) + 1, sp.feat_len, sp.feat_hist, sp.desire_len,
@@ -476,30 +484,30 @@ void ck_engine::build_plan() {
     float* fb = f32("feat_buf");
     float* tail = f32("ctx_in") + sp.temporal_dim;
     const double bytes = 10.0 * 6 * HW + 2.0 * sp.feat_hist * sp.feat_len * 4 + 2.0 * sp.feat_len * 4;
-    add("inputs", "policy_inputs", 0, bytes, [=](hipStream_t s) {
-      launch_policy_inputs(q, warped, packed, counter, ring, fr, dr, img, fb, tail, s);
-    });
+    if (head) {
+      const half_t* tw = h16("tmp.w");
+      const float* tb = f32("tmp.b");
+      float* cin = f32("ctx_in");
+      half_t* patches = h16("patches");
+      const int C0 = 6 * sp.n_frames, Kp0 = (int)round_up(9L * C0, 64);
+      const int Ho0 = (sp.img_h - 1) / 2 + 1, Wo0 = (sp.img_w - 1) / 2 + 1;
+      const double im2col_bytes = 2.0 * Ho0 * Wo0 * Kp0 * 2 + 2.0 * C0 * HW;
+      const int slots = frame_head_slots(Kt, stream_w);   // a device query: here, never under graph capture
+      add("inputs", "frame_head", tmp_flops, bytes + tmp_bytes + im2col_bytes, [=](hipStream_t s) {
+        launch_frame_head(q, warped, packed, counter, ring, fr, dr, img, fb, tail, tw, tb, cin, Td, GEMV_GELU, stream_w,
+                          patches, Kp0, slots, s);
+      });
+    } else {
+      add("inputs", "policy_inputs", 0, bytes, [=](hipStream_t s) {
+        launch_policy_inputs(q, warped, packed, counter, ring, fr, dr, img, fb, tail, s);
+      });
+    }
   }
   // The temporal and context GEMVs depend only on the feature queue: with
   // `overlap` they run on a second stream forked after the inputs, beside
   // the conv stem, and the embedding waits for them.
-  const bool overlap = sp.overlap >= 0 ? sp.overlap != 0 : false;
-  // Without the second stream the temporal GEMV shares the launch of stem
-  // layer 1's im2col (both wait only on the inputs) when its workgroups leave
-  // resident slots free: one dependent dispatch fewer, and the im2col runs in
-  // those slots beside the GEMV (39M frame -0.7%: the pair takes 11.9 us
-  // against 6.6 + 8.6).  The 1B model's GEMV alone fills every slot (768
-  // workgroups) and the shared launch leaves its frame unchanged within noise.
-  const int Kt = sp.feat_hist * sp.feat_len, Td = sp.temporal_dim;
-  bool fuse_tmp = !overlap && sp.fuse_temporal != 0;
-  int tmp_slots = 0;
-  if (fuse_tmp) {
-    tmp_slots = gemv_im2col_u8_slots(Kt, stream_w);   // a device query: here, never under graph capture
-    if (sp.fuse_temporal < 0) fuse_tmp = gemv_workgroups(Td) < tmp_slots;
-  }
-  const double tmp_flops = 2.0 * Td * Kt, tmp_bytes = (double)Td * Kt * 2 + Kt * 4 + Td * 8;
   auto add_context = [&](int branch) {
-    if (!fuse_tmp) {
+    if (!head) {
       const half_t* tw = h16("tmp.w");
       const float* tb = f32("tmp.b");
       const float* fbuf = f32("feat_buf");
@@ -568,23 +576,13 @@ void ck_engine::build_plan() {
         H = Ho; W = Wo; C = Co;
         continue;
       }
-      if (i == 0) {
+      if (i == 0 && head) {
+        // the patches come from the frame head
+      } else if (i == 0) {
         const uint8_t* img = static_cast<uint8_t*>(ptr("img"));
-        if (fuse_tmp) {
-          const half_t* tw = h16("tmp.w");
-          const float* tb = f32("tmp.b");
-          const float* fbuf = f32("feat_buf");
-          float* cin = f32("ctx_in");
-          const int slots = tmp_slots;
-          add("stem0.im2col", "gemv_im2col_u8", tmp_flops, tmp_bytes + pbytes + 2.0 * C * HW, [=](hipStream_t s) {
-            launch_gemv_im2col_u8(tw, fbuf, tb, cin, Td, Kt, GEMV_GELU, stream_w, img, 2, C, H, W, patches, Kp, slots,
-                                  s);
-          });
-        } else {
-          add("stem0.im2col", "im2col_u8", 0, pbytes + 2.0 * C * HW, [=](hipStream_t s) {
-            launch_im2col_u8(img, 2, C, H, W, patches, Kp, s);
-          });
-        }
+        add("stem0.im2col", "im2col_u8", 0, pbytes + 2.0 * C * HW, [=](hipStream_t s) {
+          launch_im2col_u8(img, 2, C, H, W, patches, Kp, s);
+        });
       } else {
         const half_t* prev = h16("stem." + std::to_string(i - 1) + ".out");
         add("stem" + si + ".im2col", "im2col_f16", 0, pbytes + 2.0 * H * W * C * 2, [=](hipStream_t s) {

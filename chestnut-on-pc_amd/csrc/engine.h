@@ -27,10 +27,10 @@ struct Spec {
   // run the temporal and context GEMVs on a second stream beside the conv
   // stem (-1: the engine decides by model size, 0: off, 1: on)
   int overlap = -1;
-  // carry the temporal GEMV in the launch of stem layer 1's im2col (-1: the
-  // engine decides (on when the GEMV leaves resident slots free), 0: off,
-  // 1: on; ignored when the context runs on its own stream)
-  int fuse_temporal = -1;
+  // run the policy inputs, the temporal GEMV and stem layer 1's im2col as one
+  // launch (1, the default; 0: three launches; ignored when the context runs
+  // on its own stream)
+  int fuse_head = 1;
   // optional per-plan-entry GEMM configuration {entry: [tile, split]} (A/B probes)
   std::vector<std::pair<std::string, std::pair<int, int>>> gemm_cfg;
 };

@@ -16,15 +16,16 @@ namespace ck {
 
 // The 8 values of thread i of batch b and their byte offset in `patches`;
 // false (nothing to store) past the end of the batch's patch matrix.
-__device__ __forceinline__ bool im2col_u8_gather(const uint8_t* __restrict__ img, int C, int H, int W, int Kp, int Ho,
-                                                 int Wo, int b, int i, half8_t& v, long& off) {
+// plane(c): the first texel of input channel c of batch b.
+template <class Plane>
+__device__ __forceinline__ bool im2col_u8_gather_p(Plane plane, int C, int H, int W, int Kp, int Ho, int Wo, int b,
+                                                   int i, half8_t& v, long& off) {
   const int kg = Kp / 8;
   const int per = Ho * Wo * kg;
   if (i >= per) return false;
   const int p = i / kg, k0 = (i - p * kg) * 8;
   const int ho = p / Wo, wo = p - ho * Wo;
   int tap = k0 / C, c = k0 - tap * C;
-  const uint8_t* base = img + (long)b * C * H * W;
   // every load is unconditional and in bounds (padding columns past the 9
   // taps re-read tap 8 and are zeroed), so all eight issue before any wait
 #pragma unroll
@@ -34,7 +35,7 @@ __device__ __forceinline__ bool im2col_u8_gather(const uint8_t* __restrict__ img
     const int fl = y * W + x;
     const int fc = min(max(fl, 0), H * W - 1);
     const bool valid = (tap < 9) & (x >= 0) & (x < W) & (y >= 0) & (y < H);
-    const uint8_t u = base[(long)c * H * W + fc];
+    const uint8_t u = plane(c)[fc];
     v[e] = (half_t)(valid ? ((float)u - 128.0f) * 0.0078125f : 0.f);
     if (++c == C) {
       c = 0;
@@ -43,6 +44,14 @@ __device__ __forceinline__ bool im2col_u8_gather(const uint8_t* __restrict__ img
   }
   off = 2L * (((long)b * Ho * Wo + p) * Kp + k0);
   return true;
+}
+
+// Planes [batch][C][H][W] in one buffer.
+__device__ __forceinline__ bool im2col_u8_gather(const uint8_t* __restrict__ img, int C, int H, int W, int Kp, int Ho,
+                                                 int Wo, int b, int i, half8_t& v, long& off) {
+  const uint8_t* base = img + (long)b * C * H * W;
+  const long hw = (long)H * W;
+  return im2col_u8_gather_p([&](int c) { return base + c * hw; }, C, H, W, Kp, Ho, Wo, b, i, v, off);
 }
 
 __device__ __forceinline__ void im2col_u8_at(const uint8_t* __restrict__ img, int C, int H, int W,

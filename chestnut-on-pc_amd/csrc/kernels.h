@@ -144,17 +144,18 @@ void launch_img_gather(const void* img, int A, int B, int lanes, int elem_bytes,
 // Conv stem im2col (zero-border reads).  Layer 1 reads normalised uint8
 // planes [batch][C][H][W]; later layers read f16 [batch][H][W][C] texels.
 void launch_im2col_u8(const uint8_t* img, int batch, int C, int H, int W, half_t* patches, int Kp, hipStream_t s);
-// launch_gemv (ldw = K, automatic row grouping) and launch_im2col_u8 in one
-// launch: two independent pieces of work that each leave part of the chip
-// idle.  `slots` = resident workgroups of the launch on the device
-// (gemv_im2col_u8_slots, queried once outside any graph capture; 0 = query
-// now); the im2col is folded onto the slots the GEMV leaves free.
-int gemv_im2col_u8_slots(int K, bool stream);
-// Workgroups of a launch_gemv with automatic row grouping over `rows` rows.
-int gemv_workgroups(int rows);
-void launch_gemv_im2col_u8(const half_t* Wt, const float* x, const float* bias, float* y, int rows, int K, int act,
-                           bool stream, const uint8_t* img, int batch, int C, int H, int W, half_t* patches, int Kp,
-                           int slots, hipStream_t s);
+// The frame's first launch: launch_policy_inputs, the temporal GEMV
+// y = act(W . features + bias) (W [rows][feat_hist*feat_len], the features
+// read from the feature ring as launch_policy_inputs samples them) and
+// launch_im2col_u8 of the sampled image (read from the image ring and
+// `warped`), in one launch.  `slots` = resident workgroups of the launch on
+// the device (frame_head_slots, queried once outside any graph capture; 0 =
+// query now): the im2col is folded onto the slots the others leave free.
+int frame_head_slots(int K, bool stream);
+void launch_frame_head(const QueueDims& q, const uint8_t* warped, const float* packed, const unsigned* counter,
+                       uint8_t* img_ring, float* feat_ring, float* desire_ring, uint8_t* img_out, float* feat_out,
+                       float* ctx_tail, const half_t* Wt, const float* bias, float* y, int rows, int act, bool stream,
+                       half_t* patches, int Kp, int slots, hipStream_t s);
 void launch_im2col_f16(const half_t* act, int batch, int C, int H, int W, half_t* patches, int Kp, hipStream_t s);
 void launch_tokens(const half_t* stem_out, int n_spatial, int C5, half_t* F, hipStream_t s);
 

@@ -407,25 +407,27 @@ def test_overlapped_context_branch_is_bit_identical(tiny, graph):
         np.testing.assert_array_equal(a, b)
 
 
-@pytest.mark.parametrize('spec_name,graph', [('tiny', True), ('tiny', False), ('driving_39m', True),
-                                             ('big_driving_1b', True)])
-def test_temporal_gemv_fused_with_stem_im2col_is_bit_identical(gpu, spec_name, graph):
-    """The temporal GEMV carried in stem layer 1's im2col launch (its
-    workgroups first, the im2col's 1024 blocks folded onto the slots it
-    leaves free: at three resident workgroups per CU, 2 blocks per workgroup
-    for tiny, 3 for 39M, 4 for 1B) gives the same bits as the two separate
-    launches, frame after frame; with the side stream on, the option is
-    ignored and the temporal GEMV keeps its own entry."""
-    sp = S.get_spec(spec_name)
+@pytest.mark.parametrize('spec_name,graph,over,nf', [('tiny', True, {}, 10), ('tiny', False, {}, 4),
+                                                     ('tiny', True, {'frame_skip': 1}, 6), ('driving_39m', True, {}, 4),
+                                                     ('big_driving_1b', True, {}, 3)],
+                         ids=['tiny-graph', 'tiny-eager', 'tiny-fs1', '39m', '1b'])
+def test_frame_head_launch_is_bit_identical(gpu, spec_name, graph, over, nf):
+    """The policy inputs, the temporal GEMV (reading the features from the
+    ring) and stem layer 1's im2col (reading the sampled frames from the
+    image ring and the staging) as one launch give the same bits as the
+    separate launches, frame after frame and through the rings' wrap-around:
+    the outputs, the sampled image, the features buffer and the patches.
+    frame_skip = 1 takes the features' last sample from the staging."""
+    sp = dict(S.get_spec(spec_name), **over)
     w = S.make_weights(sp)
-    rng = np.random.default_rng(16)
-    frames = list(frame_inputs(rng, sp, 3))
+    rng = np.random.default_rng(17)
+    frames = list(frame_inputs(rng, sp, nf))
     outs = []
-    for fuse in (0, 1):
-        with Engine(dict(sp, fuse_temporal=fuse, overlap_context=0), weights=w, graph=graph) as e:
+    for fh in (0, 1):
+        with Engine(dict(sp, fuse_head=fh), weights=w, graph=graph) as e:
             plan = {p['name']: p['kernel'] for p in e.plan()}
-            assert ('temporal' in plan) == (not fuse)
-            assert plan['stem0.im2col'] == ('gemv_im2col_u8' if fuse else 'im2col_u8')
+            assert plan['inputs'] == ('frame_head' if fh else 'policy_inputs')
+            assert ('temporal' in plan) == (not fh) and ('stem0.im2col' in plan) == (not fh)
             res, hs = [], None
             for warped, packed in frames:
                 packed = packed.copy()
@@ -433,27 +435,21 @@ def test_temporal_gemv_fused_with_stem_im2col_is_bit_identical(gpu, spec_name, g
                     packed[12:] = hs
                 o = e.run_frame(warped, packed)
                 hs = o[e.out_slices['hidden_state']]
-                res.append(o)
+                res += [o, e.read('img', np.uint8), e.read('feat_buf', np.float32), e.read('patches', np.float16),
+                        e.read('ctx_in', np.float32)]
             outs.append(res)
-    print(f'[fuse] {spec_name} graph={graph}: {len(frames)} frames compared', flush=True)
+    print(f'[head] {spec_name} {over} graph={graph}: {nf} frames compared', flush=True)
     for a, b in zip(*outs):
         np.testing.assert_array_equal(a, b)
-    if spec_name == 'tiny':
-        with Engine(dict(sp, fuse_temporal=1, overlap_context=1), weights=w, graph=graph) as e:
-            plan = {p['name']: p['kernel'] for p in e.plan()}
-            assert plan['temporal'] == 'gemv' and plan['stem0.im2col'] == 'im2col_u8'
 
 
-def test_temporal_fusion_default_follows_free_slots(gpu):
-    """By default the temporal GEMV shares the im2col launch only when its
-    workgroups leave resident slots free: the 39M model's 1664 rows (416
-    workgroups) do, the 1B model's 3072 (768, every slot at three
-    workgroups per CU) do not."""
-    for name, fused in (('driving_39m', True), ('big_driving_1b', False)):
-        with Engine(S.get_spec(name)) as e:
-            plan = {p['name']: p['kernel'] for p in e.plan()}
-        assert (plan['stem0.im2col'] == 'gemv_im2col_u8') == fused, name
-        assert ('temporal' in plan) == (not fused), name
+def test_frame_head_is_the_default_and_yields_to_the_side_stream(tiny):
+    sp, w, eng = tiny
+    plan = {p['name']: p['kernel'] for p in eng.plan()}
+    assert plan['inputs'] == 'frame_head' and 'temporal' not in plan and 'stem0.im2col' not in plan
+    with Engine(dict(sp, overlap_context=1), weights=w) as e:
+        plan = {p['name']: p['kernel'] for p in e.plan()}
+    assert plan['inputs'] == 'policy_inputs' and plan['temporal'] == 'gemv' and plan['stem0.im2col'] == 'im2col_u8'
 
 
 @pytest.mark.parametrize('spec_name', ['tiny', 'driving_39m'])
