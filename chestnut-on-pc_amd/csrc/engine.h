@@ -31,6 +31,9 @@ struct Spec {
   // launch (1, the default; 0: three launches; ignored when the context runs
   // on its own stream)
   int fuse_head = 1;
+  // with the frame head: the context GEMV rides with the last stem layer's
+  // split-K reduce launch (1, the default; 0: a launch of its own)
+  int ride_context = 1;
   // optional per-plan-entry GEMM configuration {entry: [tile, split]} (A/B probes)
   std::vector<std::pair<std::string, std::pair<int, int>>> gemm_cfg;
 };

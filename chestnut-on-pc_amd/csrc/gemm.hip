@@ -24,6 +24,7 @@
 // B column l%32, same k; D element e of lane l is row 8*(e/4) + 4*(l/32) +
 // e%4, column l%32.  The layout is checked by the MFMA KAT (wmma.hip).
 #include "common.h"
+#include "gemv_block.h"
 #include "kernels.h"
 
 namespace ck {
@@ -258,12 +259,13 @@ __global__ __launch_bounds__(256) void gemm_kernel(const GemmParams p) {
 // Sums split-K partials in split order, then applies the epilogue.  With
 // N % 4 == 0 a thread owns 4 consecutive outputs of one row (16-byte partial
 // loads); the partials of up to 8 splits are loaded before they are added.
+// Thread t of the split-K reduce: output elements t*per .. t*per+per-1.
 template <int EPI>
-__global__ __launch_bounds__(256) void splitk_reduce_kernel(const GemmParams p) {
+__device__ __forceinline__ void splitk_reduce_at(const GemmParams& p, long t) {
   const long MN = (long)p.M * p.N;
   const bool v4 = (p.N & 3) == 0;
   const int per = v4 ? 4 : 1;
-  const long idx = ((long)blockIdx.x * 256 + threadIdx.x) * per;
+  const long idx = t * per;
   if (idx >= MN * p.batch) return;
   const int bz = (int)(idx / MN);
   const long r = idx - bz * MN;
@@ -289,6 +291,24 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const GemmParams p) 
                 : static_cast<void*>(static_cast<half_t*>(p.C) + bz * p.sC);
   const float* bias = p.bias ? p.bias + bz * p.sBias : nullptr;
   for (int e = 0; e < per; ++e) epi_store<EPI>(p, C, bias, m, n + e, v[e]);
+}
+
+template <int EPI>
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const GemmParams p) {
+  splitk_reduce_at<EPI>(p, (long)blockIdx.x * 256 + threadIdx.x);
+}
+
+// The split-K reduce with an independent GEMV riding along: workgroups
+// [0, nr) reduce, the rest run the GEMV (gemv_block.h), so a small product
+// the frame needs anyway costs no launch of its own.
+template <int EPI, int NSTEP, bool NT>
+__global__ __launch_bounds__(256) void splitk_reduce_gemv_kernel(const GemmParams p, int nr, const GemvArgs g,
+                                                                 int nb) {
+  if ((int)blockIdx.x < nr) {
+    splitk_reduce_at<EPI>(p, (long)blockIdx.x * 256 + threadIdx.x);
+    return;
+  }
+  gemv_block<NSTEP, false, NT>(g, g, nb, (int)blockIdx.x - nr);
 }
 
 // ---------------------------------------------------------------------------
@@ -949,12 +969,44 @@ void launch_epi(int tile, const GemmParams& p, hipStream_t s) {
   }
 }
 
+template <int EPI, int NSTEP>
+void launch_reduce_gemv(const GemmParams& p, int nr, GemvArgs g, bool nt, hipStream_t s) {
+  g.rows_per_wg = gemv_rows_per_wg(g.rows, 0);
+  const int nb = ceil_div(g.rows, g.rows_per_wg);
+  if (nt) CK_LAUNCH((splitk_reduce_gemv_kernel<EPI, NSTEP, true>), dim3(nr + nb), dim3(256), 0, s, p, nr, g, nb);
+  else CK_LAUNCH((splitk_reduce_gemv_kernel<EPI, NSTEP, false>), dim3(nr + nb), dim3(256), 0, s, p, nr, g, nb);
+}
+
+// The split-K reduce, with the GEMV of `rider` (rows > 0) riding along.
 template <int EPI>
-void launch_reduce(const GemmParams& p, hipStream_t s) {
+void launch_reduce(const GemmParams& p, hipStream_t s, const GemvRider* rider = nullptr) {
   const long n = (long)p.M * p.N * p.batch / ((p.N & 3) == 0 ? 4 : 1);
   CK_REQUIRE((reinterpret_cast<uintptr_t>(p.ws) & 15) == 0, "gemm: split-K workspace must be 16-byte aligned");
-  CK_LAUNCH(splitk_reduce_kernel<EPI>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, p);
-  CK_LAUNCHED("splitk_reduce");
+  const int nr = (int)((n + 255) / 256);
+  if (!rider || rider->rows <= 0) {
+    CK_LAUNCH(splitk_reduce_kernel<EPI>, dim3(nr), dim3(256), 0, s, p);
+    CK_LAUNCHED("splitk_reduce");
+    return;
+  }
+  const GemvRider& r = *rider;
+  CK_REQUIRE(r.W && r.x && r.y && r.K > 0 && r.K % 8 == 0 && r.K <= 8 * GEMV_STEP_COLS,
+             "gemm: rider GEMV needs W, x, y and K a multiple of 8 up to 16384");
+  CK_REQUIRE(((reinterpret_cast<uintptr_t>(r.W) | reinterpret_cast<uintptr_t>(r.x)) & 15) == 0,
+             "gemm: rider GEMV W and x must be 16-byte aligned");
+  GemvArgs g{};
+  g.W = r.W; g.x = r.x; g.bias = r.bias; g.y = r.y;
+  g.rows = r.rows; g.K = r.K; g.ldw = r.K; g.act = GEMV_NONE;
+  switch (ceil_div(r.K, GEMV_STEP_COLS)) {
+    case 1: launch_reduce_gemv<EPI, 1>(p, nr, g, r.stream, s); break;
+    case 2: launch_reduce_gemv<EPI, 2>(p, nr, g, r.stream, s); break;
+    case 3: launch_reduce_gemv<EPI, 3>(p, nr, g, r.stream, s); break;
+    case 4: launch_reduce_gemv<EPI, 4>(p, nr, g, r.stream, s); break;
+    case 5: launch_reduce_gemv<EPI, 5>(p, nr, g, r.stream, s); break;
+    case 6: launch_reduce_gemv<EPI, 6>(p, nr, g, r.stream, s); break;
+    case 7: launch_reduce_gemv<EPI, 7>(p, nr, g, r.stream, s); break;
+    default: launch_reduce_gemv<EPI, 8>(p, nr, g, r.stream, s); break;
+  }
+  CK_LAUNCHED("splitk_reduce_gemv");
 }
 
 // A [K][N] B on the two-K-group 128x128 LDS-DMA tile is streamed into LDS as
@@ -1088,9 +1140,11 @@ void launch_gemm(GemmDesc d, hipStream_t s) {
     CK_REQUIRE(d.split == 1 && d.batch == 1 && tile_dma(d.tile) && p.vec,
                "gemm: QKV fragment epilogue needs split 1, batch 1, an LDS-DMA tile and aligned outputs");
   }
+  CK_REQUIRE(d.rider.rows <= 0 || (conv && d.split > 1),
+             "gemm: a rider GEMV goes with the split-K reduce of an implicit conv");
   if (conv) {
     launch_epi_cv<EPI_F16_BIAS_RELU>(d.tile, p, s);
-    if (d.split > 1) launch_reduce<EPI_F16_BIAS_RELU>(p, s);
+    if (d.split > 1) launch_reduce<EPI_F16_BIAS_RELU>(p, s, &d.rider);
     return;
   }
   if (d.b_kn && !tile_dma(d.tile)) {

@@ -126,11 +126,7 @@ void check_args(const GemvArgs& a) {
   CK_REQUIRE(a.act == GEMV_NONE || a.act == GEMV_GELU, "gemv: unknown activation");
 }
 
-int batch_rows(const GemvArgs& a) {
-  int rpw = a.rows_per_wg;
-  if (rpw <= 0) rpw = (a.rows + 1023) / 1024;          // >= 3 workgroups per CU up to 3072 rows
-  return ((rpw + GEMV_RB - 1) / GEMV_RB) * GEMV_RB;    // whole batches
-}
+int batch_rows(const GemvArgs& a) { return gemv_rows_per_wg(a.rows, a.rows_per_wg); }
 
 template <int NSTEP, bool GATE>
 void launch_n(GemvArgs a0, GemvArgs a1, bool two, bool nt, hipStream_t s) {

@@ -168,4 +168,11 @@ __device__ __forceinline__ void gemv_block(const GemvArgs& a0, const GemvArgs& a
   }
 }
 
+// Rows per workgroup: `rpw` rounded up to whole 4-row batches, or for rpw <= 0
+// the automatic choice, three or more workgroups per CU up to 3072 rows.
+inline int gemv_rows_per_wg(int rows, int rpw) {
+  if (rpw <= 0) rpw = (rows + 1023) / 1024;
+  return ((rpw + GEMV_RB - 1) / GEMV_RB) * GEMV_RB;
+}
+
 }  // namespace ck

@@ -42,6 +42,17 @@ enum Epi {
                           // Q, K -> C, V -> vt.  Needs head_dim, M % 32 == 0, split 1.
 };
 
+// y = W . x + bias (W f16 [rows][K], ldw = K, x f32 [K], no activation) run by
+// extra workgroups of another launch (GemmDesc::rider); rows = 0: none.
+struct GemvRider {
+  const half_t* W = nullptr;
+  const float* x = nullptr;
+  const float* bias = nullptr;
+  float* y = nullptr;
+  int rows = 0, K = 0;
+  bool stream = true;   // non-temporal weight loads (launch_gemv's `stream`)
+};
+
 struct GemmDesc {
   const half_t* A = nullptr;   // [M][K] row-major, lda
   const half_t* B = nullptr;   // [N][K] row-major (b_kn=false) or [K][N] (b_kn=true), ldb
@@ -73,6 +84,10 @@ struct GemmDesc {
   // Store the f16 result transposed, C[b*sC + n*ldc + m] (the split-K
   // reduce of EPI_F16_BIAS_RELU on tiles 1-8 only; requires split > 1).
   int c_nm = 0;
+  // A GEMV run by extra workgroups of this GEMM's split-K reduce launch
+  // (implicit conv with split > 1 only): an independent small product that
+  // then costs no launch of its own.
+  GemvRider rider;
 };
 // Resolves auto tile/split (writes them back) and returns the workspace the
 // launch needs, in floats.

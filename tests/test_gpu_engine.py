@@ -408,26 +408,32 @@ def test_overlapped_context_branch_is_bit_identical(tiny, graph):
 
 
 @pytest.mark.parametrize('spec_name,graph,over,nf', [('tiny', True, {}, 10), ('tiny', False, {}, 4),
-                                                     ('tiny', True, {'frame_skip': 1}, 6), ('driving_39m', True, {}, 4),
-                                                     ('big_driving_1b', True, {}, 3)],
-                         ids=['tiny-graph', 'tiny-eager', 'tiny-fs1', '39m', '1b'])
+                                                     ('tiny', True, {'frame_skip': 1}, 6),
+                                                     ('tiny', True, {'gemm_config': {'stem4.conv': [4, 3]}}, 4),
+                                                     ('driving_39m', True, {}, 4), ('big_driving_1b', True, {}, 3)],
+                         ids=['tiny-graph', 'tiny-eager', 'tiny-fs1', 'tiny-split-stem', '39m', '1b'])
 def test_frame_head_launch_is_bit_identical(gpu, spec_name, graph, over, nf):
     """The policy inputs, the temporal GEMV (reading the features from the
     ring) and stem layer 1's im2col (reading the sampled frames from the
-    image ring and the staging) as one launch give the same bits as the
-    separate launches, frame after frame and through the rings' wrap-around:
-    the outputs, the sampled image, the features buffer and the patches.
-    frame_skip = 1 takes the features' last sample from the staging."""
+    image ring and the staging) as one launch, and then the context GEMV
+    riding with the last stem layer's split-K reduce, give the same bits as
+    the separate launches, frame after frame and through the rings'
+    wrap-around: the outputs, the sampled image, the features buffer, the
+    patches and the context input.  frame_skip = 1 takes the features' last
+    sample from the staging."""
     sp = dict(S.get_spec(spec_name), **over)
     w = S.make_weights(sp)
     rng = np.random.default_rng(17)
     frames = list(frame_inputs(rng, sp, nf))
     outs = []
-    for fh in (0, 1):
-        with Engine(dict(sp, fuse_head=fh), weights=w, graph=graph) as e:
+    for fh, ride in ((0, 0), (1, 0), (1, 1)):
+        with Engine(dict(sp, fuse_head=fh, ride_context=ride), weights=w, graph=graph) as e:
             plan = {p['name']: p['kernel'] for p in e.plan()}
             assert plan['inputs'] == ('frame_head' if fh else 'policy_inputs')
             assert ('temporal' in plan) == (not fh) and ('stem0.im2col' in plan) == (not fh)
+            last = f"stem{len(sp['stem']) - 1}.conv"
+            rides = bool(ride) and '+splitk' in plan[last]   # the rider needs the layer's split-K reduce
+            assert ('context' in plan) == (not rides) and plan[last].endswith('+gemv') == rides
             res, hs = [], None
             for warped, packed in frames:
                 packed = packed.copy()
@@ -439,8 +445,9 @@ def test_frame_head_launch_is_bit_identical(gpu, spec_name, graph, over, nf):
                         e.read('ctx_in', np.float32)]
             outs.append(res)
     print(f'[head] {spec_name} {over} graph={graph}: {nf} frames compared', flush=True)
-    for a, b in zip(*outs):
-        np.testing.assert_array_equal(a, b)
+    for r in outs[1:]:
+        for a, b in zip(outs[0], r):
+            np.testing.assert_array_equal(a, b)
 
 
 def test_frame_head_is_the_default_and_yields_to_the_side_stream(tiny):
@@ -450,6 +457,10 @@ def test_frame_head_is_the_default_and_yields_to_the_side_stream(tiny):
     with Engine(dict(sp, overlap_context=1), weights=w) as e:
         plan = {p['name']: p['kernel'] for p in e.plan()}
     assert plan['inputs'] == 'policy_inputs' and plan['temporal'] == 'gemv' and plan['stem0.im2col'] == 'im2col_u8'
+    # the 39M model's last stem layer splits K, so the context GEMV rides with its reduce
+    with Engine(S.get_spec('driving_39m')) as e:
+        plan = {p['name']: p['kernel'] for p in e.plan()}
+    assert 'context' not in plan and plan['stem4.conv'].endswith('+splitk12+gemv')
 
 
 @pytest.mark.parametrize('spec_name', ['tiny', 'driving_39m'])
