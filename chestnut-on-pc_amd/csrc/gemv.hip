@@ -27,7 +27,10 @@
 // A launch can carry two independent GEMVs (the GRU's input and hidden
 // products: one launch instead of two), and the input vector can be the GRU
 // update computed on the fly from the gate pre-activations (the heads GEMV
-// after the GRU: the gate kernel is folded into it).
+// after the GRU: the gate kernel is folded into it).  The workgroup body
+// (gemv_block.h) also runs inside other launches: the frame head below (the
+// temporal GEMV beside the policy inputs and stem layer 1's im2col) and the
+// split-K reduce of gemm.hip (the context GEMV).
 #include <algorithm>
 
 #include "common.h"
