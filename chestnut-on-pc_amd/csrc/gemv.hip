@@ -54,10 +54,9 @@ __global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(const GemvArgs a0, c
 // reads the two sampled frames from the image ring and the staging (the
 // policy inputs' image is the same data, copied).  The policy inputs write
 // only ring slots of frame n, which neither reads.  Workgroups [0, npa) run
-// the policy inputs (short: their slots pass to the GEMV early), the next
-// nb the GEMV, the rest the im2col, folded U blocks per workgroup onto the
-// slots the others leave free, with every gather load issued before the
-// first store.
+// the policy inputs, the next nblk the im2col (both short: their slots pass
+// to the GEMV early; the im2col folded U blocks per workgroup, every gather
+// load issued before the first store), the last nb the GEMV.
 struct HeadIm2col {
   const uint8_t* warped;     // [2][6][H][W], frame n
   const uint8_t* img_ring;   // [2][img_slots][6][H][W]
@@ -69,13 +68,14 @@ struct HeadIm2col {
 template <int NSTEP, bool NT, int U>
 __global__ __launch_bounds__(GEMV_THREADS) void frame_head_kernel(const PolicyArgs pa, int npa, const GemvArgs ga,
                                                                   int nb, const HeadIm2col c) {
-  const int bid = (int)blockIdx.x;
+  int bid = (int)blockIdx.x;
   if (bid < npa) {
     policy_inputs_at(pa, (long)bid * GEMV_THREADS + threadIdx.x);
     return;
   }
-  if (bid < npa + nb) {
-    gemv_block<NSTEP, false, NT, true>(ga, ga, nb, bid - npa);
+  bid -= npa;
+  if (bid >= c.nblk) {
+    gemv_block<NSTEP, false, NT, true>(ga, ga, nb, bid - c.nblk);
     return;
   }
   constexpr int C = 12;   // two sampled 6-channel frames
@@ -90,7 +90,7 @@ __global__ __launch_bounds__(GEMV_THREADS) void frame_head_kernel(const PolicyAr
 #pragma unroll
   for (int u = 0; u < U; ++u) {
     // clamped to the last valid block and item (their stores are dropped)
-    const int j0 = bid - nb - npa + u * c.nblk, j = min(j0, total - 1);
+    const int j0 = bid + u * c.nblk, j = min(j0, total - 1);
     const int b = j / c.blocks_per_image;
     const int i0 = (j - b * c.blocks_per_image) * GEMV_THREADS + (int)threadIdx.x, i = min(i0, per - 1);
     const uint8_t* old_frame = c.img_ring + ((long)b * c.img_slots + old_slot) * fb;
