@@ -57,9 +57,9 @@ __global__ __launch_bounds__(256) void layernorm_kernel(float* __restrict__ x, c
   }
 }
 
-// Wide rows (d >= 512): one 256-thread workgroup per row.  Thread t owns the
-// VW-wide chunks t, t+256, ... (VW = 4, or 2 for d = 512), so every access is
-// a coalesced 8/16-byte vector.  All loads -- x, every split-K partial (up to
+// Wide rows (d >= 1024; d = 512 has the wave form below): one 256-thread
+// workgroup per row.  Thread t owns the VW-wide chunks t, t+256, ... (VW = 4,
+// or 2 for d = 512), so every access is a coalesced 8/16-byte vector.  All loads -- x, every split-K partial (up to
 // LN_MAXS), the bias, gamma and beta -- are issued before any arithmetic: one
 // memory round trip per row instead of one per partial.  Per element the
 // residual update is x + ((((ws0 + ws1) + ws2) + ...) + bias), in split
@@ -159,6 +159,94 @@ __global__ __launch_bounds__(256) void layernorm_row_kernel(float* __restrict__ 
   }
 }
 
+// d = 512 (the 39M model): one 64-lane wave per row, a workgroup each.
+// Lane l owns the 16-byte chunks l and l + 64, loaded with every partial,
+// the bias, gamma and beta before any arithmetic; the same per-element
+// residual order as the row kernel; row sums by DPP wave sums alone (no LDS,
+// no barrier).
+template <bool OUT_F16, int NS>
+__global__ __launch_bounds__(64) void layernorm_wave_kernel(float* __restrict__ x, const float* __restrict__ ws,
+                                                            int nsplit, long split_stride,
+                                                            const float* __restrict__ rbias,
+                                                            const float* __restrict__ g, const float* __restrict__ b,
+                                                            void* __restrict__ out, float eps) {
+  constexpr int NV = 2, D = NV * 256;
+  const int row = blockIdx.x, lane = threadIdx.x;
+  float* xr = x + (long)row * D;
+  float4_t v[NV], gv[NV], bv[NV];
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int c = (j * 64 + lane) * 4;
+    v[j] = *reinterpret_cast<const float4_t*>(xr + c);
+    gv[j] = *reinterpret_cast<const float4_t*>(g + c);
+    bv[j] = *reinterpret_cast<const float4_t*>(b + c);
+  }
+  if (NS != 0) {
+    constexpr int KN = NS > 0 ? NS : LN_MAXS;
+    float4_t p[KN][NV], rb[NV];
+    const float* w = ws + (long)row * D;
+#pragma unroll
+    for (int k = 0; k < KN; ++k)
+#pragma unroll
+      for (int j = 0; j < NV; ++j)
+        p[k][j] = (NS > 0 || k < nsplit) ? *reinterpret_cast<const float4_t*>(w + k * split_stride + (j * 64 + lane) * 4)
+                                         : float4_t{};
+#pragma unroll
+    for (int j = 0; j < NV; ++j) rb[j] = rbias ? *reinterpret_cast<const float4_t*>(rbias + (j * 64 + lane) * 4) : float4_t{};
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      float4_t a = p[0][j];
+#pragma unroll
+      for (int k = 1; k < KN; ++k)
+        if (NS > 0 || k < nsplit) a += p[k][j];
+      if (rbias) a += rb[j];
+      v[j] = v[j] + a;
+      store_sc1(sc1_rsrc(xr, 4L * D), 4L * (j * 64 + lane) * 4, v[j]);
+    }
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) s += (v[j][0] + v[j][1]) + (v[j][2] + v[j][3]);
+  const float mean = wave_sum(s) / (float)D;
+  float q = 0.f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float c = v[j][e] - mean;
+      q = fmaf(c, c, q);
+    }
+  const float rstd = 1.0f / sqrtf(wave_sum(q) / (float)D + eps);
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int c = (j * 64 + lane) * 4;
+    float4_t y;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) y[e] = (v[j][e] - mean) * rstd * gv[j][e] + bv[j][e];
+    if (OUT_F16)
+      store_sc1(sc1_rsrc(static_cast<half_t*>(out) + (long)row * D, 2L * D), 2L * c,
+                half4_t{(half_t)y[0], (half_t)y[1], (half_t)y[2], (half_t)y[3]});
+    else
+      store_sc1(sc1_rsrc(static_cast<float*>(out) + (long)row * D, 4L * D), 4L * c, y);
+  }
+}
+
+void ln_wave_launch(float* x, const float* ws, int nsplit, long sstride, const float* rbias, const float* g,
+                    const float* b, void* out, bool f16, int rows, float eps, hipStream_t s) {
+  auto go = [&](auto ns) {
+    constexpr int NS = decltype(ns)::value;
+    if (f16) CK_LAUNCH((layernorm_wave_kernel<true, NS>), dim3(rows), dim3(64), 0, s, x, ws, nsplit, sstride, rbias, g, b, out, eps);
+    else CK_LAUNCH((layernorm_wave_kernel<false, NS>), dim3(rows), dim3(64), 0, s, x, ws, nsplit, sstride, rbias, g, b, out, eps);
+  };
+  if (!ws) go(std::integral_constant<int, 0>{});
+  else if (nsplit == 1) go(std::integral_constant<int, 1>{});
+  else if (nsplit == 2) go(std::integral_constant<int, 2>{});
+  else if (nsplit == 4) go(std::integral_constant<int, 4>{});
+  else if (nsplit == 8) go(std::integral_constant<int, 8>{});
+  else go(std::integral_constant<int, -1>{});
+  CK_LAUNCHED("layernorm_wave");
+}
+
 template <int EPT>
 void ln_row_launch(float* x, const float* ws, int nsplit, long sstride, const float* rbias, const float* g,
                    const float* b, void* out, bool f16, int rows, float eps, hipStream_t s) {
@@ -250,7 +338,7 @@ void launch_add_layernorm(float* x, const float* ws, int nsplit, long split_stri
   switch (d) {
     case 128: ln_launch<2>(x, ws, nsplit, split_stride, rbias, g, b, out, out_f16, rows, eps, s); break;
     case 256: ln_launch<4>(x, ws, nsplit, split_stride, rbias, g, b, out, out_f16, rows, eps, s); break;
-    case 512: ln_row_launch<2>(x, ws, nsplit, split_stride, rbias, g, b, out, out_f16, rows, eps, s); break;
+    case 512: ln_wave_launch(x, ws, nsplit, split_stride, rbias, g, b, out, out_f16, rows, eps, s); break;
     case 1024: ln_row_launch<4>(x, ws, nsplit, split_stride, rbias, g, b, out, out_f16, rows, eps, s); break;
     case 2048: ln_row_launch<8>(x, ws, nsplit, split_stride, rbias, g, b, out, out_f16, rows, eps, s); break;
     default: throw Error("layernorm: d must be one of 128, 256, 512, 1024, 2048");
