@@ -51,11 +51,14 @@ constexpr int att_waves(int nkt) { return nkt <= 4 ? 2 * nkt : nkt; }
 // GEMM's fragment epilogue): every fragment load of a wave is one contiguous
 // KB.  Otherwise the row layouts: qk [T][2d], vt [d][T].  All of a wave's
 // loads (Q, its K, its V) are issued at entry, before any MFMA.
-template <int HD, int NKT, bool FRAG>
+// QT: 16-query tiles per workgroup (2: 32 queries; 1: 16, twice the
+// workgroups for short sequences that would leave most CUs idle).
+template <int HD, int NKT, bool FRAG, int QT = 2>
 __global__ __launch_bounds__(64 * att_waves(NKT)) void attention_kernel(const half_t* __restrict__ qk,
                                                                          const half_t* __restrict__ vt,
                                                                          half_t* __restrict__ out, int n_heads,
                                                                          float scale_log2e) {
+  constexpr int QB = 16 * QT;        // queries per workgroup
   constexpr int WAVES = att_waves(NKT);
   constexpr int T = 64 * NKT;
   constexpr int KS = HD / 32;        // k-steps of the q.k products
@@ -65,22 +68,22 @@ __global__ __launch_bounds__(64 * att_waves(NKT)) void attention_kernel(const ha
   constexpr int CT = HD / 16;        // 16-wide output tiles
   constexpr int OP = HD + 4;         // partial-output row pitch (floats)
   static_assert(KPW % 32 == 0, "every wave must own whole 32-key blocks");
-  __shared__ __attribute__((aligned(16))) float part[WAVES][ATT_QB][OP];
-  __shared__ float mrow[WAVES][ATT_QB], lrow[WAVES][ATT_QB];
+  __shared__ __attribute__((aligned(16))) float part[WAVES][QB][OP];
+  __shared__ float mrow[WAVES][QB], lrow[WAVES][QB];
 
   const int d = n_heads * HD;
-  const int nqb = T / ATT_QB;
+  const int nqb = T / QB;
   const int total = nqb * n_heads;
   int L = blockIdx.x;
   if ((total & 7) == 0) L = (L & 7) * (total >> 3) + (L >> 3);
-  const int h = L / nqb, q0 = (L % nqb) * ATT_QB;
+  const int h = L / nqb, q0 = (L % nqb) * QB;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r16 = lane & 15, g = lane >> 4;
   const long ldq = 2L * d;
   const int kw0 = wave * KPW;
 
   // ---- all loads up front ----
-  half8_t qf[2][KS], kf[KT][KS], vb[KB][CT];
+  half8_t qf[QT][KS], kf[KT][KS], vb[KB][CT];
 #pragma unroll
   for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
@@ -89,7 +92,7 @@ __global__ __launch_bounds__(64 * att_waves(NKT)) void attention_kernel(const ha
           FRAG ? qk + ((((long)(n_heads + h) * (T / 16) + kw0 / 16 + kt) * KS + ks) * 64 + lane) * 8
                : qk + (long)(kw0 + kt * 16 + r16) * ldq + d + h * HD + ks * 32 + g * 8);
 #pragma unroll
-  for (int qt = 0; qt < 2; ++qt)
+  for (int qt = 0; qt < QT; ++qt)
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks)
       qf[qt][ks] = *reinterpret_cast<const half8_t*>(
@@ -112,11 +115,11 @@ __global__ __launch_bounds__(64 * att_waves(NKT)) void attention_kernel(const ha
     }
 
   // ---- 1. S^T = K Q^T for this wave's keys (log2 domain) ----
-  float4_t s[KT][2];
+  float4_t s[KT][QT];
 #pragma unroll
   for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
-    for (int qt = 0; qt < 2; ++qt) {
+    for (int qt = 0; qt < QT; ++qt) {
       float4_t a = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) a = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[kt][ks], qf[qt][ks], a, 0, 0, 0);
@@ -124,9 +127,9 @@ __global__ __launch_bounds__(64 * att_waves(NKT)) void attention_kernel(const ha
     }
 
   // ---- 2. wave-local softmax numerator per query (column r16 of q-tile qt) ----
-  half8_t pa[KB][2];
+  half8_t pa[KB][QT];
 #pragma unroll
-  for (int qt = 0; qt < 2; ++qt) {
+  for (int qt = 0; qt < QT; ++qt) {
     float m = -INFINITY;
 #pragma unroll
     for (int kt = 0; kt < KT; ++kt)
@@ -150,9 +153,9 @@ __global__ __launch_bounds__(64 * att_waves(NKT)) void attention_kernel(const ha
   }
 
   // ---- 3. O_w = e V over this wave's keys ----
-  float4_t o[2][CT];
+  float4_t o[QT][CT];
 #pragma unroll
-  for (int qt = 0; qt < 2; ++qt)
+  for (int qt = 0; qt < QT; ++qt)
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) {
       float4_t a = {0.f, 0.f, 0.f, 0.f};
@@ -161,7 +164,7 @@ __global__ __launch_bounds__(64 * att_waves(NKT)) void attention_kernel(const ha
       o[qt][ct] = a;
     }
 #pragma unroll
-  for (int qt = 0; qt < 2; ++qt)
+  for (int qt = 0; qt < QT; ++qt)
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct)
 #pragma unroll
@@ -169,7 +172,7 @@ __global__ __launch_bounds__(64 * att_waves(NKT)) void attention_kernel(const ha
   __syncthreads();
 
   // ---- 4. combine the waves: 4 features of one query per step, in fixed wave order ----
-  for (int u = threadIdx.x; u < ATT_QB * HD / 4; u += 64 * WAVES) {
+  for (int u = threadIdx.x; u < QB * HD / 4; u += 64 * WAVES) {
     const int q = u / (HD / 4), c = (u % (HD / 4)) * 4;
     float M = mrow[0][q];
 #pragma unroll
@@ -191,9 +194,15 @@ __global__ __launch_bounds__(64 * att_waves(NKT)) void attention_kernel(const ha
 
 template <int HD, int NKT, bool FRAG>
 void launch_t(int n_heads, const half_t* qk, const half_t* vt, half_t* out, float scale_log2e, hipStream_t s) {
-  const dim3 grid((64 * NKT / ATT_QB) * n_heads);
-  CK_LAUNCH((attention_kernel<HD, NKT, FRAG>), grid, dim3(64 * att_waves(NKT)), 0, s, qk, vt, out, n_heads,
-                     scale_log2e);
+  // 32 queries per workgroup, or 16 when that would leave more than half the CUs idle
+  const int wg32 = (64 * NKT / ATT_QB) * n_heads;
+  if (wg32 >= 128) {
+    CK_LAUNCH((attention_kernel<HD, NKT, FRAG, 2>), dim3(wg32), dim3(64 * att_waves(NKT)), 0, s, qk, vt, out, n_heads,
+              scale_log2e);
+  } else {
+    CK_LAUNCH((attention_kernel<HD, NKT, FRAG, 1>), dim3(2 * wg32), dim3(64 * att_waves(NKT)), 0, s, qk, vt, out,
+              n_heads, scale_log2e);
+  }
 }
 
 template <int HD, bool FRAG>
