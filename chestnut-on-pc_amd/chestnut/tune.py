@@ -92,9 +92,13 @@ def config_for(sp, choice):
     return cfg
 
 
-def time_frames(sp, weights, frames=100, warmup=10):
+def time_frames(sp, weights, frames=100, warmup=10, names=None):
+    """ms per frame of back-to-back graph launches; `names`, a list, receives
+    the plan's entry names."""
     from .engine import Engine
     with Engine(sp, weights=weights) as eng:
+        if names is not None:
+            names.extend(e['name'] for e in eng.plan())
         rng = np.random.default_rng(42)
         w = rng.integers(0, 256, (2, 6, sp['img_h'], sp['img_w']), dtype=np.uint8)
         p = np.zeros(sp['desire_len'] + 4 + sp['feat_len'], np.float32)
@@ -120,11 +124,16 @@ def tune(spec='big_driving_1b', families=FAMILIES, frames=100, log=print):
     # the first engine of a process runs slower (about 0.6% on the 1B model:
     # clocks and allocations settle), so the defaults are timed twice and
     # the second run is the baseline
-    time_frames(sp, weights, frames)
+    present = []
+    time_frames(sp, weights, frames, names=present)
     base = time_frames(sp, weights, frames)
     log(f'[tune] {sp["name"]}: engine defaults {base:.4f} ms/frame')
     best_ms, table = base, [('defaults', base)]
     for fam in families:
+        if not all(n in present for n in entry_names(sp, fam)):
+            # e.g. the O-projection where it runs inside the attention launch
+            log(f'[tune] {fam}: no such GEMM in this plan, skipped')
+            continue
         M, N, K, kind, batch = shp[fam]
         best_c = None
         for c in candidates(M, N, K, kind, batch):

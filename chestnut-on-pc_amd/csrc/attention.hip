@@ -53,11 +53,22 @@ constexpr int att_waves(int nkt) { return nkt <= 4 ? 2 * nkt : nkt; }
 // loads (Q, its K, its V) are issued at entry, before any MFMA.
 // QT: 16-query tiles per workgroup (2: 32 queries; 1: 16, twice the
 // workgroups for short sequences that would leave most CUs idle).
-template <int HD, int NKT, bool FRAG, int QT = 2>
+// OTW > 0: the output projection rides along.  The workgroup's normalised
+// f16 output (QB queries x HD features of head h) goes to LDS instead of
+// memory, and wave w multiplies it by columns [h*HD, (h+1)*HD) of W_o
+// ([d][d], row n = output feature) for output features
+// [16*OTW*w, 16*OTW*(w+1)): P_h = O_h W_o[:, h]^T, an f32 plane per head,
+// opart + h*T*d, [T][d].  The planes are the split-K partials of the
+// O-projection over its K = d split by heads; the next LayerNorm sums them
+// in head order with the bias.  W_o's fragments are loaded at entry with
+// everything else.
+template <int HD, int NKT, bool FRAG, int QT = 2, int OTW = 0>
 __global__ __launch_bounds__(64 * att_waves(NKT)) void attention_kernel(const half_t* __restrict__ qk,
                                                                          const half_t* __restrict__ vt,
                                                                          half_t* __restrict__ out, int n_heads,
-                                                                         float scale_log2e) {
+                                                                         float scale_log2e,
+                                                                         const half_t* __restrict__ wo,
+                                                                         float* __restrict__ opart) {
   constexpr int QB = 16 * QT;        // queries per workgroup
   constexpr int WAVES = att_waves(NKT);
   constexpr int T = 64 * NKT;
@@ -70,6 +81,9 @@ __global__ __launch_bounds__(64 * att_waves(NKT)) void attention_kernel(const ha
   static_assert(KPW % 32 == 0, "every wave must own whole 32-key blocks");
   __shared__ __attribute__((aligned(16))) float part[WAVES][QB][OP];
   __shared__ float mrow[WAVES][QB], lrow[WAVES][QB];
+  constexpr int KSO = HD / 32;       // k-steps of the O-projection
+  constexpr int OBP = HD + 8;        // f16 output row pitch in LDS (16-byte rows)
+  __shared__ __attribute__((aligned(16))) half_t ob[OTW > 0 ? QB : 1][OBP];
 
   const int d = n_heads * HD;
   const int nqb = T / QB;
@@ -113,6 +127,16 @@ __global__ __launch_bounds__(64 * att_waves(NKT)) void attention_kernel(const ha
         vb[kb][ct] = half8_t{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
       }
     }
+  // W_o fragments (MFMA A operand: row n = output feature, 8 k of head h's columns)
+  half8_t wf[OTW > 0 ? OTW : 1][KSO];
+  if constexpr (OTW > 0) {
+#pragma unroll
+    for (int t = 0; t < OTW; ++t)
+#pragma unroll
+      for (int ks = 0; ks < KSO; ++ks)
+        wf[t][ks] = *reinterpret_cast<const half8_t*>(wo + (long)((wave * OTW + t) * 16 + r16) * d + h * HD +
+                                                      ks * 32 + g * 8);
+  }
 
   // ---- 1. S^T = K Q^T for this wave's keys (log2 domain) ----
   float4_t s[KT][QT];
@@ -186,9 +210,36 @@ __global__ __launch_bounds__(64 * att_waves(NKT)) void attention_kernel(const ha
       acc += f * *reinterpret_cast<const float4_t*>(&part[w][q][c]);
     }
     const float rden = 1.0f / den;
-    // device-scope cache policy for the output the O-projection reads next (-0.4% of the 1B frame)
-    store_sc1(sc1_rsrc(out, 2L * T * d), ((long)(q0 + q) * d + h * HD + c) * 2,
-              half4_t{(half_t)(acc[0] * rden), (half_t)(acc[1] * rden), (half_t)(acc[2] * rden), (half_t)(acc[3] * rden)});
+    const half4_t v{(half_t)(acc[0] * rden), (half_t)(acc[1] * rden), (half_t)(acc[2] * rden), (half_t)(acc[3] * rden)};
+    if constexpr (OTW > 0) {
+      *reinterpret_cast<half4_t*>(&ob[q][c]) = v;
+    } else {
+      // device-scope cache policy for the output the O-projection reads next (-0.4% of the 1B frame)
+      store_sc1(sc1_rsrc(out, 2L * T * d), ((long)(q0 + q) * d + h * HD + c) * 2, v);
+    }
+  }
+
+  // ---- 5. (OTW > 0) P_h^T = W_o[n-tile, head h] O_h^T: lane (g, r16) ends with
+  // output features 4g..4g+3 of the tile for query r16, one 16-byte store ----
+  if constexpr (OTW > 0) {
+    __syncthreads();
+    half8_t of[QT][KSO];
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+      for (int ks = 0; ks < KSO; ++ks)
+        of[qt][ks] = *reinterpret_cast<const half8_t*>(&ob[qt * 16 + r16][ks * 32 + g * 8]);
+    const auto pr = sc1_rsrc(opart + (long)h * T * d, 4L * T * d);
+#pragma unroll
+    for (int t = 0; t < OTW; ++t)
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt) {
+        float4_t a = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < KSO; ++ks) a = __builtin_amdgcn_mfma_f32_16x16x32_f16(wf[t][ks], of[qt][ks], a, 0, 0, 0);
+        // device-scope cache policy: the LayerNorm reads the planes next
+        store_sc1(pr, ((long)(q0 + qt * 16 + r16) * d + (wave * OTW + t) * 16 + 4 * g) * 4, a);
+      }
   }
 }
 
@@ -198,10 +249,50 @@ void launch_t(int n_heads, const half_t* qk, const half_t* vt, half_t* out, floa
   const int wg32 = (64 * NKT / ATT_QB) * n_heads;
   if (wg32 >= 128) {
     CK_LAUNCH((attention_kernel<HD, NKT, FRAG, 2>), dim3(wg32), dim3(64 * att_waves(NKT)), 0, s, qk, vt, out, n_heads,
-              scale_log2e);
+              scale_log2e, nullptr, nullptr);
   } else {
     CK_LAUNCH((attention_kernel<HD, NKT, FRAG, 1>), dim3(2 * wg32), dim3(64 * att_waves(NKT)), 0, s, qk, vt, out,
-              n_heads, scale_log2e);
+              n_heads, scale_log2e, nullptr, nullptr);
+  }
+}
+
+// With the O-projection: the same workgroup choice; OTW = d / 16 / waves
+// output tiles per wave (checked by attention_oproj_tiles).
+template <int HD, int NKT, int OTW>
+void launch_o(int n_heads, const half_t* qk, const half_t* vt, const half_t* wo, float* opart, float scale_log2e,
+              hipStream_t s) {
+  const int wg32 = (64 * NKT / ATT_QB) * n_heads;
+  if (wg32 >= 128) {
+    CK_LAUNCH((attention_kernel<HD, NKT, true, 2, OTW>), dim3(wg32), dim3(64 * att_waves(NKT)), 0, s, qk, vt, nullptr,
+              n_heads, scale_log2e, wo, opart);
+  } else {
+    CK_LAUNCH((attention_kernel<HD, NKT, true, 1, OTW>), dim3(2 * wg32), dim3(64 * att_waves(NKT)), 0, s, qk, vt,
+              nullptr, n_heads, scale_log2e, wo, opart);
+  }
+}
+
+template <int HD, int NKT>
+void launch_o_t(int otw, int n_heads, const half_t* qk, const half_t* vt, const half_t* wo, float* opart,
+                float scale_log2e, hipStream_t s) {
+  switch (otw) {
+    case 1: launch_o<HD, NKT, 1>(n_heads, qk, vt, wo, opart, scale_log2e, s); break;
+    case 2: launch_o<HD, NKT, 2>(n_heads, qk, vt, wo, opart, scale_log2e, s); break;
+    default: launch_o<HD, NKT, 4>(n_heads, qk, vt, wo, opart, scale_log2e, s); break;
+  }
+}
+
+template <int HD>
+void launch_o_hd(int T, int otw, int n_heads, const half_t* qk, const half_t* vt, const half_t* wo, float* opart,
+                 float scale_log2e, hipStream_t s) {
+  switch (T / 64) {
+    case 1: launch_o_t<HD, 1>(otw, n_heads, qk, vt, wo, opart, scale_log2e, s); break;
+    case 2: launch_o_t<HD, 2>(otw, n_heads, qk, vt, wo, opart, scale_log2e, s); break;
+    case 3: launch_o_t<HD, 3>(otw, n_heads, qk, vt, wo, opart, scale_log2e, s); break;
+    case 4: launch_o_t<HD, 4>(otw, n_heads, qk, vt, wo, opart, scale_log2e, s); break;
+    case 5: launch_o_t<HD, 5>(otw, n_heads, qk, vt, wo, opart, scale_log2e, s); break;
+    case 6: launch_o_t<HD, 6>(otw, n_heads, qk, vt, wo, opart, scale_log2e, s); break;
+    case 7: launch_o_t<HD, 7>(otw, n_heads, qk, vt, wo, opart, scale_log2e, s); break;
+    default: launch_o_t<HD, 8>(otw, n_heads, qk, vt, wo, opart, scale_log2e, s); break;
   }
 }
 
@@ -241,6 +332,31 @@ void launch_attention(const half_t* qk, const half_t* vt, half_t* out, int T, in
     else launch_hd<128, false>(T, n_heads, qk, vt, out, scale_log2e, s);
   }
   CK_LAUNCHED("attention");
+}
+
+int attention_oproj_tiles(int T, int n_heads, int head_dim) {
+  if (T <= 0 || T % 64 != 0 || T > ATT_TMAX || (head_dim != 64 && head_dim != 128) || n_heads <= 0) return 0;
+  const int tiles = n_heads * head_dim / 16, waves = att_waves(T / 64);
+  if (tiles % waves != 0) return 0;
+  const int otw = tiles / waves;
+  return (otw == 1 || otw == 2 || otw == 4) ? otw : 0;
+}
+
+void launch_attention_oproj(const half_t* qk, const half_t* vt, const half_t* wo, float* opart, int T, int n_heads,
+                            int head_dim, hipStream_t s) {
+  CK_REQUIRE(qk && vt && wo && opart, "attention_oproj: null pointer");
+  const int otw = attention_oproj_tiles(T, n_heads, head_dim);
+  CK_REQUIRE(otw > 0,
+             "attention_oproj: needs T a multiple of 64 up to 512, head_dim 64 or 128, and 1, 2 or 4 output "
+             "tiles of 16 features per wave");
+  CK_REQUIRE(4L * T * n_heads * head_dim < (1L << 31), "attention_oproj: partial plane too large");
+  CK_REQUIRE(((reinterpret_cast<uintptr_t>(qk) | reinterpret_cast<uintptr_t>(vt) | reinterpret_cast<uintptr_t>(wo) |
+               reinterpret_cast<uintptr_t>(opart)) & 15) == 0,
+             "attention_oproj: operands must be 16-byte aligned");
+  const float scale_log2e = 1.4426950408889634f / sqrtf((float)head_dim);
+  if (head_dim == 64) launch_o_hd<64>(T, otw, n_heads, qk, vt, wo, opart, scale_log2e, s);
+  else launch_o_hd<128>(T, otw, n_heads, qk, vt, wo, opart, scale_log2e, s);
+  CK_LAUNCHED("attention_oproj");
 }
 
 }  // namespace ck

@@ -96,6 +96,7 @@ Spec parse_spec(const std::string& json) {
   s.overlap = jint(o, "overlap_context", -1);
   s.fuse_head = jint(o, "fuse_head", 1);
   s.ride_context = jint(o, "ride_context", 1);
+  s.fuse_oproj = jint(o, "fuse_oproj", -1);
   if (const JVal* gc = o.get("gemm_config")) {
     CK_REQUIRE(gc->kind == JVal::OBJ, "spec: gemm_config must be an object {entry: [tile, split]}");
     for (const auto& kv : gc->obj) {
@@ -666,6 +667,12 @@ void ck_engine::build_plan() {
   const int s_dn = small(d) ? resid_split(T, d, F, 64, 64, 64, 256) : resid_split(T, d, F, 128, 128, 128, 512);
   ck_engine* self = this;
   const long part_stride = (long)T * d;
+  // attention + O-projection in one launch: one partial plane per head
+  const bool oproj_ok = attention_oproj_tiles(T, sp.n_heads, sp.head_dim) > 0 && sp.n_heads <= 8;
+  CK_REQUIRE(sp.fuse_oproj != 1 || oproj_ok,
+             "spec: fuse_oproj needs at most 8 heads and a shape the fused attention takes");
+  const bool fuse_o = sp.fuse_oproj == 1 || (sp.fuse_oproj < 0 && oproj_ok);
+  if (fuse_o) ws_floats = std::max(ws_floats, (size_t)sp.n_heads * T * d);
   const float* pend_bias = nullptr;   // bias of the GEMM whose partials the next LN must add
   int pend_split = 0;
   auto add_ln = [&](const std::string& name, const float* g, const float* bb, void* out, bool f16) {
@@ -697,13 +704,23 @@ void ck_engine::build_plan() {
     const half_t* vt = h16("vt");
     half_t* att = h16("att");
     const int nh = sp.n_heads, hd = sp.head_dim, Tt = T;
-    add(b + "attn", "attention", 4.0 * Tt * Tt * d, (double)Tt * d * 2 * 4, [=](hipStream_t s) {
-      launch_attention(qk, vt, att, Tt, nh, hd, true, s);
-    });
-    GemmDesc o;
-    o.A = att; o.lda = d; o.B = h16(p + "o.w"); o.ldb = d;
-    o.M = T; o.N = d; o.K = d; o.epi = EPI_PARTIALS; o.tile = tile_o; o.split = s_o;   // 64x128 (64x64 when small)
-    pend_split = add_gemm(b + "o", "gemm_partials", o);   // the split actually used (gemm_config may set it)
+    if (fuse_o) {
+      // the head-h plane of the O-projection comes out of head h's attention
+      // workgroups; the LayerNorm adds the n_heads planes in head order
+      const half_t* wo = h16(p + "o.w");
+      add(b + "attn", "attention_oproj", 4.0 * Tt * Tt * d + 2.0 * Tt * d * d,
+          (double)Tt * d * 2 * 3 + (double)d * d * 2 + (double)nh * Tt * d * 4,
+          [=](hipStream_t s) { launch_attention_oproj(qk, vt, wo, self->ws, Tt, nh, hd, s); });
+      pend_split = nh;
+    } else {
+      add(b + "attn", "attention", 4.0 * Tt * Tt * d, (double)Tt * d * 2 * 4, [=](hipStream_t s) {
+        launch_attention(qk, vt, att, Tt, nh, hd, true, s);
+      });
+      GemmDesc o;
+      o.A = att; o.lda = d; o.B = h16(p + "o.w"); o.ldb = d;
+      o.M = T; o.N = d; o.K = d; o.epi = EPI_PARTIALS; o.tile = tile_o; o.split = s_o;   // 64x128 (64x64 when small)
+      pend_split = add_gemm(b + "o", "gemm_partials", o);   // the split actually used (gemm_config may set it)
+    }
     pend_bias = f32(p + "o.b");
     add_ln(b + "ln2", f32(p + "ln2.g"), f32(p + "ln2.b"), hb, true);
     GemmDesc up;

@@ -34,6 +34,11 @@ struct Spec {
   // with the frame head: the context GEMV rides with the last stem layer's
   // split-K reduce launch (1, the default; 0: a launch of its own)
   int ride_context = 1;
+  // attention and the output projection in one launch, the projection's
+  // per-head f32 partials summed by the next LayerNorm (-1, the default: where
+  // the heads fit the LayerNorm's 8 partials and the kernel takes the shape;
+  // 0: off; 1: on, an error where it cannot be)
+  int fuse_oproj = -1;
   // optional per-plan-entry GEMM configuration {entry: [tile, split]} (A/B probes)
   std::vector<std::pair<std::string, std::pair<int, int>>> gemm_cfg;
 };

@@ -101,6 +101,14 @@ void launch_gemm(GemmDesc d, hipStream_t s);
 // Non-causal softmax(q k^T * scale) v per head.
 void launch_attention(const half_t* qk, const half_t* vt, half_t* out, int T, int n_heads, int head_dim, bool frag,
                       hipStream_t s);
+// Attention (fragment layout) with the output projection in the same launch:
+// opart + h*T*d = O_h W_o[:, h*hd:(h+1)*hd]^T, f32 [T][d], one plane per head
+// (the O-projection's partials over K split by heads, summed by the next
+// LayerNorm); wo f16 [d][d].  attention_oproj_tiles returns the output tiles
+// per wave for a shape (0: not supported, use launch_attention + a GEMM).
+int attention_oproj_tiles(int T, int n_heads, int head_dim);
+void launch_attention_oproj(const half_t* qk, const half_t* vt, const half_t* wo, float* opart, int T, int n_heads,
+                            int head_dim, hipStream_t s);
 
 // ---- normalisation / small elementwise ---------------------------------------
 void launch_layernorm(const float* x, const float* g, const float* b, void* out, bool out_f16, int rows,
