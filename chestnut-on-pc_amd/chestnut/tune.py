@@ -94,11 +94,11 @@ def config_for(sp, choice):
 
 def time_frames(sp, weights, frames=100, warmup=10, names=None):
     """ms per frame of back-to-back graph launches; `names`, a list, receives
-    the plan's entry names."""
+    the names of the plan's GEMM entries."""
     from .engine import Engine
     with Engine(sp, weights=weights) as eng:
         if names is not None:
-            names.extend(e['name'] for e in eng.plan())
+            names.extend(e['name'] for e in eng.plan() if e['kernel'].startswith('gemm'))
         rng = np.random.default_rng(42)
         w = rng.integers(0, 256, (2, 6, sp['img_h'], sp['img_w']), dtype=np.uint8)
         p = np.zeros(sp['desire_len'] + 4 + sp['feat_len'], np.float32)
