@@ -35,6 +35,8 @@ def _expect(kernel):
         return 'gemv'
     if 'layernorm' in k:
         return 'layernorm'
+    if k.startswith('attention'):   # attention, attention_oproj: one attention_kernel
+        return 'attention'
     return k
 
 

@@ -49,6 +49,16 @@ def test_frames_reject_mismatch(tmp_path):
     assert P.frames_from_trace(P.load_trace(tmp_path / 't.csv'), PLAN) == []
 
 
+def test_fused_attention_entry_matches_the_attention_kernel(tmp_path):
+    # attention with the O-projection inside is one attention_kernel dispatch
+    plan = [{'name': 'blk0.attn', 'kernel': 'attention_oproj', 'flops': 1, 'bytes': 1},
+            {'name': 'blk0.ln2', 'kernel': 'add_layernorm_f16', 'flops': 0, 'bytes': 1}]
+    seq = [('_ZN2ck12_GLOBAL__N_116attention_kernelILi64ELi4ELb1ELi1ELi4EEEvPKDF16_', 3.0),
+           ('layernorm_wave_kernel<true, 8>', 2.0)]
+    _trace_csv(tmp_path / 't.csv', seq)
+    assert P.frames_from_trace(P.load_trace(tmp_path / 't.csv'), plan) == [[3.0, 2.0]]
+
+
 def test_frames_md_families(tmp_path):
     _trace_csv(tmp_path / 't.csv', FRAME)
     with open(tmp_path / 's.csv', 'w', newline='') as fh:
