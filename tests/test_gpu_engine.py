@@ -469,8 +469,18 @@ def test_frame_head_is_the_default_and_yields_to_the_side_stream(tiny):
     assert 'context' not in plan and plan['stem4.conv'].endswith('+splitk12+gemv')
 
 
-@pytest.mark.parametrize('spec_name,nf', [('tiny', 8), ('driving_39m', 4)])
-def test_attention_oproj_fusion(gpu, spec_name, nf):
+# shapes of the fused kernel beyond the two models: head_dim 128; 32-query
+# workgroups (T = 512, 8 heads); 2 and 1 output tiles per wave
+OPROJ_SHAPES = [('tiny', {}, 8), ('driving_39m', {}, 4),
+                ('tiny', dict(stem=[8, 16, 32, 64, 128], d_model=256, n_heads=2, head_dim=128), 3),
+                ('tiny', dict(stem=[8, 16, 32, 64, 512], d_model=512, n_heads=8, head_dim=64, d_ff=1024), 2),
+                ('tiny', dict(stem=[8, 16, 32, 64, 128]), 3),
+                ('tiny', dict(stem=[8, 16, 32, 64, 512]), 2)]
+
+
+@pytest.mark.parametrize('spec_name,over,nf', OPROJ_SHAPES,
+                         ids=['tiny', '39m', 'hd128', 'q32-T512', 'otw2', 'otw1'])
+def test_attention_oproj_fusion(gpu, spec_name, over, nf):
     """Attention with the output projection in the same launch (one f32
     plane per head, P_h = O_h W_o[:, head h]^T, summed by the next LayerNorm
     in head order) is the default where the heads fit the LayerNorm's 8
@@ -478,7 +488,7 @@ def test_attention_oproj_fusion(gpu, spec_name, nf):
     within the north-star bound of the oracle, and within f32 rounding of
     attention followed by a split-K O-projection GEMM (the same products,
     summed in another grouping)."""
-    sp = S.get_spec(spec_name)
+    sp = dict(S.get_spec(spec_name), **over)
     w = S.make_weights(sp)
     orc = OM.OracleModel(sp, w, acc=np.float64)
     rng = np.random.default_rng(23)
@@ -509,7 +519,7 @@ def test_attention_oproj_fusion(gpu, spec_name, nf):
     for a, b in zip(outs[-1], outs[0]):
         for sl in slices.values():
             worst = max(worst, rel_err(a[sl], b[sl].astype(np.float64)))
-    print(f'[oproj] {spec_name}: {nf} frames, fused vs GEMM worst rel {worst:.2e}', flush=True)
+    print(f'[oproj] {spec_name} {over}: {nf} frames, fused vs GEMM worst rel {worst:.2e}', flush=True)
     assert worst <= 1e-4
 
 
