@@ -47,6 +47,75 @@ __global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(const GemvArgs a0, c
   gemv_block<NSTEP, GATE, NT>(a0, a1, nb0, (int)blockIdx.x);
 }
 
+// K <= 512: one wave spans a row (lane l: columns 8l..8l+7), so the four
+// waves of a workgroup take rows of their own, RW each, all loaded at once,
+// and a row's sum is the wave sum alone: no LDS combine and no barrier (the
+// workgroup form leaves three of its four waves without columns at these K).
+// The lane's products and the wave sum are the workgroup form's, and the
+// other waves' zero partials added there are exact, so y is the same.
+constexpr int GEMV_WAVE_RW = 2;   // rows per wave
+template <bool GATE, bool NT>
+__global__ __launch_bounds__(GEMV_THREADS) void gemv_wave_kernel(const GemvArgs a0, const GemvArgs a1, int nb0) {
+  constexpr int RW = GEMV_WAVE_RW;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const bool second = (int)blockIdx.x >= nb0;
+  const GemvArgs& a = second ? a1 : a0;
+  const int blk = second ? (int)blockIdx.x - nb0 : (int)blockIdx.x;
+  const int K = a.K, c = lane * 8, cc = min(c, K - 8);   // columns past K read the last chunk, times x = 0
+  const int r0 = (blk * 4 + wave) * RW;
+  if (r0 >= a.rows) return;   // whole wave; nothing below waits on other waves
+  half8_t w[RW];
+#pragma unroll
+  for (int i = 0; i < RW; ++i) {
+    const half8_t* p = reinterpret_cast<const half8_t*>(a.W + (long)min(r0 + i, a.rows - 1) * a.ldw + cc);
+    w[i] = NT ? __builtin_nontemporal_load(p) : *p;
+  }
+  float xr[8];
+  if (GATE) {
+    const float* src[7] = {a.gi + cc, a.gi + K + cc, a.gi + 2 * K + cc, a.gh + cc, a.gh + K + cc, a.gh + 2 * K + cc,
+                           a.hp + cc};
+    float4_t g[7][2];
+#pragma unroll
+    for (int q = 0; q < 7; ++q) {
+      g[q][0] = *reinterpret_cast<const float4_t*>(src[q]);
+      g[q][1] = *reinterpret_cast<const float4_t*>(src[q] + 4);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int h = j >> 2, e = j & 3;
+      const float r = sigmoidf_(g[0][h][e] + g[3][h][e]);
+      const float z = sigmoidf_(g[1][h][e] + g[4][h][e]);
+      const float n = tanhf(g[2][h][e] + r * g[5][h][e]);
+      xr[j] = c < K ? (1.0f - z) * n + z * g[6][h][e] : 0.f;
+    }
+    if (blk == 0 && wave == 0 && c < K) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        a.h1[c + j] = xr[j];
+        if (a.h2) a.h2[c + j] = xr[j];
+      }
+    }
+  } else {
+    const float4_t u = *reinterpret_cast<const float4_t*>(a.x + cc);
+    const float4_t v = *reinterpret_cast<const float4_t*>(a.x + cc + 4);
+    const bool in = c < K;
+    xr[0] = in ? u[0] : 0.f; xr[1] = in ? u[1] : 0.f; xr[2] = in ? u[2] : 0.f; xr[3] = in ? u[3] : 0.f;
+    xr[4] = in ? v[0] : 0.f; xr[5] = in ? v[1] : 0.f; xr[6] = in ? v[2] : 0.f; xr[7] = in ? v[3] : 0.f;
+  }
+#pragma unroll
+  for (int i = 0; i < RW; ++i) {
+    float v = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v = fmaf((float)w[i][j], xr[j], v);
+    v = wave_sum(v);
+    if (lane == i && r0 + i < a.rows) {
+      if (a.bias) v += a.bias[r0 + i];
+      if (a.act == GEMV_GELU) v = gelu_tanh(v);
+      a.y[r0 + i] = v;
+    }
+  }
+}
+
 // The frame's first launch: the policy inputs (policy_inputs.h), the
 // temporal GEMV and stem layer 1's im2col, which need nothing from each
 // other: the GEMV reads the features where they lie in the feature ring (the
@@ -149,6 +218,15 @@ void launch_n(GemvArgs a0, GemvArgs a1, bool two, bool nt, hipStream_t s) {
 
 template <bool GATE>
 void launch_args(const GemvArgs& a0, const GemvArgs& a1, bool two, bool nt, hipStream_t s) {
+  if (a0.K <= 512 && (!two || a1.K <= 512) && a0.rows_per_wg <= 0 && (!two || a1.rows_per_wg <= 0) && !a0.xring) {
+    constexpr int per = 4 * GEMV_WAVE_RW;   // rows per workgroup
+    const int nb0 = ceil_div(a0.rows, per);
+    const int grid = nb0 + (two ? ceil_div(a1.rows, per) : 0);
+    if (nt) CK_LAUNCH((gemv_wave_kernel<GATE, true>), dim3(grid), dim3(GEMV_THREADS), 0, s, a0, two ? a1 : a0, nb0);
+    else CK_LAUNCH((gemv_wave_kernel<GATE, false>), dim3(grid), dim3(GEMV_THREADS), 0, s, a0, two ? a1 : a0, nb0);
+    CK_LAUNCHED("gemv_wave");
+    return;
+  }
   const int nstep = ceil_div(two ? std::max(a0.K, a1.K) : a0.K, GEMV_STEP_COLS);
   switch (nstep) {
     case 1: launch_n<1, GATE>(a0, a1, two, nt, s); break;
