@@ -106,7 +106,8 @@ def test_gemv_config2_full_size(gpu):
         np.testing.assert_array_equal(host(K.gemv(Wd, xd, rows_per_wg=rpw)), y)
 
 
-@pytest.mark.parametrize('rows,Kd,act', [(1, 8, 0), (7, 3280, 0), (1536, 2048, 1), (1673, 512, 0), (5, 16384, 1)])
+@pytest.mark.parametrize('rows,Kd,act', [(1, 8, 0), (7, 3280, 0), (1536, 2048, 1), (1673, 512, 0), (5, 16384, 1),
+                                         (37, 136, 1)])
 def test_gemv_shapes_bias_act(gpu, rows, Kd, act):
     from chestnut import kernels as K
     rng = np.random.default_rng(rows + Kd)
@@ -120,6 +121,22 @@ def test_gemv_shapes_bias_act(gpu, rows, Kd, act):
     if act:
         bound = bound * 1.2 + 4 * U * np.abs(ref)
     assert np.all(np.abs(y - ref) <= bound)
+
+
+@pytest.mark.parametrize('rows,Kd,act', [(1, 8, 0), (9, 136, 1), (1673, 512, 0)])
+def test_gemv_wave_form_matches_workgroup_form(gpu, rows, Kd, act):
+    """K <= 512 with the automatic row partition runs one wave per row; a
+    pinned rows_per_wg runs the workgroup form.  The lane products and the
+    wave sum are the same and the workgroup form's extra partials are exact
+    zeros, so the two agree bit for bit."""
+    from chestnut import kernels as K
+    rng = np.random.default_rng(7 * rows + Kd)
+    W = dev(gpu, (rng.standard_normal((rows, Kd)) * 0.05).astype(np.float16))
+    x = dev(gpu, rng.uniform(-1, 1, Kd).astype(np.float32))
+    b = dev(gpu, rng.standard_normal(rows).astype(np.float32))
+    y = host(K.gemv(W, x, b, act=act))
+    for rpw in (4, 8):
+        np.testing.assert_array_equal(host(K.gemv(W, x, b, act=act, rows_per_wg=rpw)), y)
 
 
 # ---------------------------------------------------------------- GEMM ----
