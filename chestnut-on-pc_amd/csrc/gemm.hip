@@ -391,23 +391,43 @@ __device__ __forceinline__ void dma_issue(const half_t* const* asrc, const half_
 //   16+4g..16+4g+3 of a 32-token block, the attention kernel's key order):
 //     vt chunk ((h * hd/16 + j/16) * T/32 + t/32) * 64 + 16*((t%16)/4) + j%16,
 //     element (t/16)*4 + t%4 of the chunk.
-template <int WM, int WN, int FM, int FN, int EPI>
+// SWP (every epilogue but the QKV ones): the accumulators hold D^T (the MFMA
+// ran with its operands swapped), so element e of tile (i, j) is row
+// i*32 + lane%32, column j*32 + 8*(e/4) + 4*(lane/32) + e%4: a lane's four
+// consecutive e are four consecutive columns of one row, staged with one 8-
+// or 16-byte LDS write instead of four scalar ones; bcol[j][e] is the bias
+// of that column (bcol[j][0] of column j*32 + lane%32 otherwise).
+template <int WM, int WN, int FM, int FN, int EPI, bool SWP, int NBC>
 __device__ __forceinline__ void store_staged(const GemmParams& p, const float16_t (&acc)[FM][FN],
-                                             const float (&bcol)[FN], char* region, int mw, int nw, int sp, int bz,
-                                             int lane) {
+                                             const float (&bcol)[FN][NBC], char* region, int mw, int nw, int sp,
+                                             int bz, int lane) {
   const bool to_ws = p.split > 1 || EPI == EPI_PARTIALS;
   if (to_ws || EPI == EPI_F32 || EPI == EPI_F32_RESID || EPI == EPI_EMBED) {
     constexpr int PF = WN + 8;   // floats
     float* st = reinterpret_cast<float*>(region);
+    if constexpr (SWP) {
 #pragma unroll
-    for (int j = 0; j < FN; ++j) {
-      const int c = j * 32 + (lane & 31);
-      const float bv = bcol[j];
+      for (int j = 0; j < FN; ++j)
 #pragma unroll
-      for (int i = 0; i < FM; ++i)
+        for (int i = 0; i < FM; ++i)
 #pragma unroll
-        for (int e = 0; e < 16; ++e)
-          st[(i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3)) * PF + c] = acc[i][j][e] + bv;
+          for (int k = 0; k < 4; ++k) {
+            float4_t v;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = acc[i][j][4 * k + e] + bcol[j][4 * k + e];
+            *reinterpret_cast<float4_t*>(st + (i * 32 + (lane & 31)) * PF + j * 32 + 8 * k + 4 * (lane >> 5)) = v;
+          }
+    } else {
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        const int c = j * 32 + (lane & 31);
+        const float bv = bcol[j][0];
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+          for (int e = 0; e < 16; ++e)
+            st[(i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3)) * PF + c] = acc[i][j][e] + bv;
+      }
     }
     __builtin_amdgcn_wave_barrier();
     asm volatile("" ::: "memory");
@@ -441,7 +461,7 @@ __device__ __forceinline__ void store_staged(const GemmParams& p, const float16_
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
       const int c = j * 32 + (lane & 31);
-      const float bv = bcol[j];
+      const float bv = bcol[j][0];
 #pragma unroll
       for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -491,19 +511,38 @@ __device__ __forceinline__ void store_staged(const GemmParams& p, const float16_
     return;
   }
   constexpr int PH = WN + 8;   // halves
+  if constexpr (SWP) {
 #pragma unroll
-  for (int j = 0; j < FN; ++j) {
-    const int c = j * 32 + (lane & 31);
-    const float bv = bcol[j];
+    for (int j = 0; j < FN; ++j)
 #pragma unroll
-    for (int i = 0; i < FM; ++i)
+      for (int i = 0; i < FM; ++i)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        float v = acc[i][j][e] + bv;
-        if (EPI == EPI_F16_BIAS_RELU) v = fmaxf(v, 0.f);
-        if (EPI == EPI_F16_BIAS_GELU) v = gelu_fast(v);
-        st[(i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3)) * PH + c] = (half_t)v;
-      }
+        for (int k = 0; k < 4; ++k) {
+          half4_t hv;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            float v = acc[i][j][4 * k + e] + bcol[j][4 * k + e];
+            if (EPI == EPI_F16_BIAS_RELU) v = fmaxf(v, 0.f);
+            if (EPI == EPI_F16_BIAS_GELU) v = gelu_fast(v);
+            hv[e] = (half_t)v;
+          }
+          *reinterpret_cast<half4_t*>(st + (i * 32 + (lane & 31)) * PH + j * 32 + 8 * k + 4 * (lane >> 5)) = hv;
+        }
+  } else {
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      const int c = j * 32 + (lane & 31);
+      const float bv = bcol[j][0];
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          float v = acc[i][j][e] + bv;
+          if (EPI == EPI_F16_BIAS_RELU) v = fmaxf(v, 0.f);
+          if (EPI == EPI_F16_BIAS_GELU) v = gelu_fast(v);
+          st[(i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3)) * PH + c] = (half_t)v;
+        }
+    }
   }
   __builtin_amdgcn_wave_barrier();
   asm volatile("" ::: "memory");
@@ -662,14 +701,20 @@ __global__ __launch_bounds__(64 * NWG * KG) void gemm_dma_kernel(const GemmParam
   // the bias of the lane's epilogue columns, loaded before the K loop so its
   // latency hides behind the loop (older than every DMA, it has landed by the
   // first vmcnt wait)
-  float bcol[FN];
+  // every epilogue but the QKV ones runs the MFMA with swapped operands
+  // (accumulators = D^T; see store_staged)
+  constexpr bool SWP = EPI != EPI_QKV && EPI != EPI_QKV_FRAG;
+  constexpr int NBC = SWP ? 16 : 1;
+  float bcol[FN][NBC];
   {
     const float* bias = (p.split == 1 && EPI != EPI_PARTIALS && p.bias) ? p.bias + bz * p.sBias : nullptr;
 #pragma unroll
-    for (int j = 0; j < FN; ++j) {
-      const int n = n0 + wn * WN + j * 32 + (lane & 31);
-      bcol[j] = (bias && n < p.N) ? bias[n] : 0.f;
-    }
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int e = 0; e < NBC; ++e) {
+        const int n = n0 + wn * WN + j * 32 + (SWP ? 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3) : (lane & 31));
+        bcol[j][e] = (bias && n < p.N) ? bias[n] : 0.f;
+      }
   }
 
   // group step t is global step KG*t + grp, held in ring stage (KG*t + grp) % S
@@ -768,7 +813,8 @@ __global__ __launch_bounds__(64 * NWG * KG) void gemm_dma_kernel(const GemmParam
       for (int i = 0; i < FM; ++i)
 #pragma unroll
         for (int j = 0; j < FN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[kk][i], bf[kk][j], acc[i][j], 0, 0, 0);
+          acc[i][j] = SWP ? __builtin_amdgcn_mfma_f32_32x32x16_f16(bf[kk][j], af[kk][i], acc[i][j], 0, 0, 0)
+                          : __builtin_amdgcn_mfma_f32_32x32x16_f16(af[kk][i], bf[kk][j], acc[i][j], 0, 0, 0);
       if (kk + 2 < KS) read_slice(kk + 2);
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -809,7 +855,7 @@ __global__ __launch_bounds__(64 * NWG * KG) void gemm_dma_kernel(const GemmParam
   if (p.vec) {
     constexpr int REGION = WM * (WN + 8) * 4;   // bytes per wave; the f32 staging is the largest
     static_assert(NWG * REGION <= S * STAGE * 2, "LDS ring too small for the staged epilogue");
-    store_staged<WM, WN, FM, FN, EPI>(p, acc, bcol, reinterpret_cast<char*>(lds) + w4 * REGION, m0 + wm * WM,
+    store_staged<WM, WN, FM, FN, EPI, SWP, NBC>(p, acc, bcol, reinterpret_cast<char*>(lds) + w4 * REGION, m0 + wm * WM,
                                       n0 + wn * WN, sp, bz, lane);
     return;
   }
@@ -822,8 +868,8 @@ __global__ __launch_bounds__(64 * NWG * KG) void gemm_dma_kernel(const GemmParam
       for (int j = 0; j < FN; ++j)
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
-          const int m = m0 + wm * WM + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
-          const int n = n0 + wn * WN + j * 32 + (lane & 31);
+          const int m = m0 + wm * WM + i * 32 + (SWP ? (lane & 31) : 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3));
+          const int n = n0 + wn * WN + j * 32 + (SWP ? 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3) : (lane & 31));
           if (m < p.M && n < p.N) ws[(long)m * p.N + n] = acc[i][j][e];
         }
     return;
@@ -838,8 +884,8 @@ __global__ __launch_bounds__(64 * NWG * KG) void gemm_dma_kernel(const GemmParam
     for (int j = 0; j < FN; ++j)
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
-        const int m = m0 + wm * WM + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
-        const int n = n0 + wn * WN + j * 32 + (lane & 31);
+        const int m = m0 + wm * WM + i * 32 + (SWP ? (lane & 31) : 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3));
+        const int n = n0 + wn * WN + j * 32 + (SWP ? 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3) : (lane & 31));
         if (m < p.M && n < p.N) epi_store<EPI>(p, C, bias, m, n, acc[i][j][e]);
       }
 }
