@@ -701,11 +701,15 @@ __global__ __launch_bounds__(64 * NWG * KG) void gemm_dma_kernel(const GemmParam
   // the bias of the lane's epilogue columns, loaded before the K loop so its
   // latency hides behind the loop (older than every DMA, it has landed by the
   // first vmcnt wait)
-  // every epilogue but the QKV ones runs the MFMA with swapped operands
-  // (accumulators = D^T; see store_staged), except on the [K][N] B path,
-  // whose transposed B reads measured slower in the other operand slot
-  // (config 1: 33.2 against 32.3 us)
-  constexpr bool SWP = EPI != EPI_QKV && EPI != EPI_QKV_FRAG && !BT;
+  // the epilogues of the tiles with two or more 32x32 products per wave run
+  // the MFMA with swapped operands (accumulators = D^T; see store_staged),
+  // except the QKV ones and the [K][N] B path, whose transposed B reads
+  // measured slower in the other operand slot (config 1: 33.2 against
+  // 32.3 us).  On the 64x64 tiles (one product per wave) the 16 bias values
+  // per lane cost more than the staging writes save (39M frame 0.1870 ->
+  // 0.1907 ms); the 1B model's O-projection (two per wave) gains (1B frame
+  // 2.047 -> 2.036 ms).
+  constexpr bool SWP = EPI != EPI_QKV && EPI != EPI_QKV_FRAG && !BT && FM * FN >= 2;
   constexpr int NBC = SWP ? 16 : 1;
   float bcol[FN][NBC];
   {
