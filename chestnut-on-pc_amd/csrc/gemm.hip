@@ -290,6 +290,32 @@ __device__ __forceinline__ void splitk_reduce_at(const GemmParams& p, long t) {
                 ? static_cast<void*>(static_cast<float*>(p.C) + bz * p.sC)
                 : static_cast<void*>(static_cast<half_t*>(p.C) + bz * p.sC);
   const float* bias = p.bias ? p.bias + bz * p.sBias : nullptr;
+  // Row-major outputs take the thread's 4 values in one 16-byte (f32) or
+  // 8-byte (f16) store where the address allows: the same values as
+  // epi_store, a quarter of the store instructions.
+  if (v4 && (EPI == EPI_F32 || ((EPI == EPI_F16_BIAS || EPI == EPI_F16_BIAS_RELU || EPI == EPI_F16_BIAS_GELU) &&
+                                !p.c_nm))) {
+    float o[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      o[e] = bias ? v[e] + bias[n + e] : v[e];
+      if (EPI == EPI_F16_BIAS_RELU) o[e] = fmaxf(o[e], 0.f);
+      if (EPI == EPI_F16_BIAS_GELU) o[e] = gelu_fast(o[e]);
+    }
+    if (EPI == EPI_F32) {
+      float* c = static_cast<float*>(C) + (long)m * p.ldc + n;
+      if ((reinterpret_cast<uintptr_t>(c) & 15) == 0) {
+        *reinterpret_cast<float4_t*>(c) = float4_t{o[0], o[1], o[2], o[3]};
+        return;
+      }
+    } else {
+      half_t* c = static_cast<half_t*>(C) + (long)m * p.ldc + n;
+      if ((reinterpret_cast<uintptr_t>(c) & 7) == 0) {
+        *reinterpret_cast<half4_t*>(c) = half4_t{(half_t)o[0], (half_t)o[1], (half_t)o[2], (half_t)o[3]};
+        return;
+      }
+    }
+  }
   for (int e = 0; e < per; ++e) epi_store<EPI>(p, C, bias, m, n + e, v[e]);
 }
 
