@@ -209,9 +209,14 @@ def layernorm(x, g, b, eps=1e-5, out_f16=True):
     return out
 
 
-def warp_nv12(frame, big_frame, tfm, big_tfm, cam_w, cam_h, stride, y_height, model_w=512, model_h=256, out=None):
+def warp_nv12(frame, big_frame, tfm, big_tfm, cam_w, cam_h, stride, y_height, model_w=512, model_h=256, out=None,
+              division='ieee'):
     """NV12 frames (u8 device buffers) + f32 [3,3] inverse transforms ->
-    u8 [2, 6, model_h/2, model_w/2] (the engine's `warped`)."""
+    u8 [2, 6, model_h/2, model_w/2] (the engine's `warped`).  division:
+    'ieee' (src_x / src_w) or 'rcp' (src_x * (1 / src_w)), as
+    oracle.warp's `div`."""
+    if division not in ('ieee', 'rcp'):
+        raise ValueError("division must be 'ieee' or 'rcp'")
     nb = stride * y_height + (cam_h // 2) * stride
     for t, n in ((frame, 'frame'), (big_frame, 'big_frame')):
         if t.numel() != nb:
@@ -226,5 +231,5 @@ def warp_nv12(frame, big_frame, tfm, big_tfm, cam_w, cam_h, stride, y_height, mo
     if out is None:
         out = torch.empty(shape, dtype=torch.uint8, device=frame.device)
     call('ck_warp_nv12', _ptr(frame), _ptr(big_frame), frame.numel(), _ptr(tfm), _ptr(big_tfm), cam_w, cam_h, stride,
-         y_height, model_w, model_h, _ptr(out), _stream())
+         y_height, model_w, model_h, 1 if division == 'rcp' else 0, _ptr(out), _stream())
     return out

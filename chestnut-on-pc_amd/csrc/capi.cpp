@@ -238,6 +238,13 @@ int ck_kernel_times(ck_engine* e, float* ms, int n) {
   CK_API_END
 }
 
+int ck_state_hashes(ck_engine* e, uint64_t* out, int n) {
+  CK_API_BEGIN
+  CK_REQUIRE(e && out, "null argument");
+  e->state_hashes(out, n);
+  CK_API_END
+}
+
 int ck_run_range(ck_engine* e, int first, int last) {
   CK_API_BEGIN
   CK_REQUIRE(e, "null engine");
@@ -385,10 +392,10 @@ int ck_img_gather(const void* img, int A, int B, int lanes, int elem_bytes, cons
 
 int ck_warp_nv12(const uint8_t* frame, const uint8_t* big_frame, size_t frame_bytes, const float* tfm,
                  const float* big_tfm, int cam_w, int cam_h, int stride, int y_height, int model_w, int model_h,
-                 uint8_t* out, void* stream) {
+                 int division, uint8_t* out, void* stream) {
   CK_API_BEGIN
-  launch_warp_nv12(frame, big_frame, frame_bytes, tfm, big_tfm, cam_w, cam_h, stride, y_height, model_w, model_h, out,
-                   as_stream(stream));
+  launch_warp_nv12(frame, big_frame, frame_bytes, tfm, big_tfm, cam_w, cam_h, stride, y_height, model_w, model_h,
+                   division, out, as_stream(stream));
   CK_API_END
 }
 

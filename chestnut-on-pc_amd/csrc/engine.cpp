@@ -89,6 +89,11 @@ Spec parse_spec(const std::string& json) {
     s.cam_h = jint(*cam, "height", 0, true);
     s.cam_stride = jint(*cam, "stride", 0, true);
     s.cam_y_height = jint(*cam, "y_height", 0, true);
+    if (const JVal* dv = cam->get("division")) {
+      CK_REQUIRE(dv->kind == JVal::STR && (dv->str == "ieee" || dv->str == "rcp"),
+                 "spec: camera.division must be \"ieee\" or \"rcp\"");
+      s.cam_div = dv->str == "rcp";
+    }
     CK_REQUIRE(s.cam_w > 0 && s.cam_h > 0 && s.cam_w % 2 == 0 && s.cam_h % 2 == 0 && s.cam_stride >= s.cam_w &&
                    s.cam_y_height >= s.cam_h,
                "spec: camera needs an even width and height, stride >= width, y_height >= height");
@@ -97,6 +102,7 @@ Spec parse_spec(const std::string& json) {
   s.fuse_head = jint(o, "fuse_head", 1);
   s.ride_context = jint(o, "ride_context", 1);
   s.fuse_oproj = jint(o, "fuse_oproj", -1);
+  s.graph_upload = jint(o, "graph_upload", 0);
   if (const JVal* gc = o.get("gemm_config")) {
     CK_REQUIRE(gc->kind == JVal::OBJ, "spec: gemm_config must be an object {entry: [tile, split]}");
     for (const auto& kv : gc->obj) {
@@ -190,6 +196,11 @@ void ck_engine::release() noexcept {
   by_name.clear();
   plan.clear();
   if (dec_dev) (void)hipFree(dec_dev);
+  if (hash_spans_dev) (void)hipFree(hash_spans_dev);
+  if (hash_part_dev) (void)hipFree(hash_part_dev);
+  hash_spans_dev = nullptr;
+  hash_part_dev = nullptr;
+  hash_spans.clear();
   if (h_warped) (void)hipHostFree(h_warped);
   if (h_packed) (void)hipHostFree(h_packed);
   if (h_out) (void)hipHostFree(h_out);
@@ -865,6 +876,10 @@ void ck_engine::capture() {
   CK_HIP(hipStreamEndCapture(stream, &graph));
   CK_HIP(hipGraphGetNodes(graph, nullptr, &graph_nodes));
   CK_HIP(hipGraphInstantiate(&gexec, graph, nullptr, nullptr, 0));
+  if (sp.graph_upload) {
+    CK_HIP(hipGraphUpload(gexec, stream));
+    CK_HIP(hipStreamSynchronize(stream));
+  }
 }
 
 void ck_engine::frame_launch() {
@@ -916,7 +931,7 @@ void ck_engine::run_frame_nv12(const uint8_t* frame, const uint8_t* big_frame, c
   CK_HIP(hipMemcpyAsync(tf, h_tfm, 18 * sizeof(float), hipMemcpyHostToDevice, stream));
   CK_HIP(hipMemcpyAsync(ptr("packed"), h_packed, packed_len * sizeof(float), hipMemcpyHostToDevice, stream));
   launch_warp_nv12(nv, nv + nv12_bytes, nv12_bytes, tf, tf + 9, sp.cam_w, sp.cam_h, sp.cam_stride, sp.cam_y_height,
-                   2 * sp.img_w, 2 * sp.img_h, static_cast<uint8_t*>(ptr("warped")), stream);
+                   2 * sp.img_w, 2 * sp.img_h, sp.cam_div, static_cast<uint8_t*>(ptr("warped")), stream);
   frame_launch();
   CK_HIP(hipMemcpyAsync(h_out, ptr("out"), n_out * sizeof(float), hipMemcpyDeviceToHost, stream));
   CK_HIP(hipStreamSynchronize(stream));
@@ -935,6 +950,31 @@ void ck_engine::run_range(int first, int last) {
   CK_REQUIRE(first >= 0 && last <= (int)plan.size() && first <= last, "run_range: bad plan range");
   for (int i = first; i < last; ++i) plan[i].fn(stream);
   CK_HIP(hipStreamSynchronize(stream));
+}
+
+void ck_engine::state_hashes(uint64_t* out, int n) {
+  std::vector<const Tensor*> st;
+  for (const auto& t : tensors)
+    if (!t.param) st.push_back(&t);
+  CK_REQUIRE(n >= (int)st.size(), "state_hashes: output array shorter than the state tensor count");
+  if (!hash_part_dev) {
+    for (int i = 0; i < (int)st.size(); ++i)
+      for (size_t off = 0; off < st[i]->nbytes; off += HASH_SPAN_BYTES)
+        hash_spans.push_back({static_cast<const uint8_t*>(st[i]->ptr), (long)off,
+                              (int)std::min<size_t>(HASH_SPAN_BYTES, st[i]->nbytes - off), i});
+    CK_REQUIRE(!hash_spans.empty(), "state_hashes: no state bytes");
+    CK_HIP(hipMalloc(&hash_spans_dev, hash_spans.size() * sizeof(HashSpan)));
+    CK_HIP(hipMalloc(&hash_part_dev, hash_spans.size() * sizeof(unsigned long long)));
+    CK_HIP(hipMemcpy(hash_spans_dev, hash_spans.data(), hash_spans.size() * sizeof(HashSpan),
+                     hipMemcpyHostToDevice));
+  }
+  launch_state_hash(hash_spans_dev, (int)hash_spans.size(), hash_part_dev, stream);
+  std::vector<unsigned long long> part(hash_spans.size());
+  CK_HIP(hipMemcpyAsync(part.data(), hash_part_dev, part.size() * sizeof(unsigned long long), hipMemcpyDeviceToHost,
+                        stream));
+  CK_HIP(hipStreamSynchronize(stream));
+  for (int i = 0; i < (int)st.size(); ++i) out[i] = hash_mix(st[i]->nbytes);
+  for (size_t k = 0; k < hash_spans.size(); ++k) out[hash_spans[k].tensor] += part[k];
 }
 
 void ck_engine::kernel_times(float* ms, int n) {

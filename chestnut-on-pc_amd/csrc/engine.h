@@ -24,6 +24,8 @@ struct Spec {
   std::vector<std::pair<std::string, int>> outputs;
   // optional NV12 camera geometry (run_frame_nv12); width 0 = none
   int cam_w = 0, cam_h = 0, cam_stride = 0, cam_y_height = 0;
+  // the warp's coordinate division: 0 "ieee" src_x / src_w, 1 "rcp" src_x * (1 / src_w)
+  int cam_div = 0;
   // run the temporal and context GEMVs on a second stream beside the conv
   // stem (-1: the engine decides by model size, 0: off, 1: on)
   int overlap = -1;
@@ -39,6 +41,9 @@ struct Spec {
   // the heads fit the LayerNorm's 8 partials and the kernel takes the shape;
   // 0: off; 1: on, an error where it cannot be)
   int fuse_oproj = -1;
+  // graph instantiation: 0 default; 1 upload the executable graph to the
+  // engine stream (hipGraphUpload) before its first launch
+  int graph_upload = 0;
   // optional per-plan-entry GEMM configuration {entry: [tile, split]} (A/B probes)
   std::vector<std::pair<std::string, std::pair<int, int>>> gemm_cfg;
 };
@@ -80,6 +85,10 @@ struct ck_engine {
   size_t graph_nodes = 0;
   float* ws = nullptr;
   size_t ws_floats = 0;
+  // state hashing (ck_state_hashes): span table and per-span partials, built on first use
+  std::vector<ck::HashSpan> hash_spans;
+  ck::HashSpan* hash_spans_dev = nullptr;
+  unsigned long long* hash_part_dev = nullptr;
   // output decode: per-head table (host + device copy), decoded-vector layout as JSON
   std::vector<ck::DecodeHead> dec_heads;
   ck::DecodeHead* dec_dev = nullptr;
@@ -116,6 +125,9 @@ struct ck_engine {
   void kernel_times(float* ms, int n);
   float time_launches(const int* idx, int n, int reps);
   float time_in_frames(const int* idx, int n, int frames, float* per_entry_ms);
+  // hash of every state tensor (non-parameter, allocation order), after the
+  // work already queued on the engine stream
+  void state_hashes(uint64_t* out, int n);
 
  private:
   void init();

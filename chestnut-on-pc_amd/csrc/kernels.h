@@ -141,9 +141,11 @@ void launch_decode(const float* raw, float* decoded, const DecodeHead* heads_dev
 // frame, big_frame: NV12 (Y plane of y_height rows, then the interleaved UV
 // plane), rows of `stride` bytes, frame_bytes each; tfm, big_tfm: device f32
 // [3][3] inverse transforms; out u8 [2][6][model_h/2][model_w/2].
+// division: 0 src_x / src_w (correctly rounded quotient), 1 src_x * (1 / src_w)
+// (correctly rounded reciprocal, then the product).
 void launch_warp_nv12(const uint8_t* frame, const uint8_t* big_frame, size_t frame_bytes, const float* tfm,
                       const float* big_tfm, int cam_w, int cam_h, int stride, int y_height, int model_w, int model_h,
-                      uint8_t* out, hipStream_t s);
+                      int division, uint8_t* out, hipStream_t s);
 
 // ---- frame inputs, packing, image2d ------------------------------------------
 struct QueueDims {
@@ -181,6 +183,19 @@ void launch_frame_head(const QueueDims& q, const uint8_t* warped, const float* p
                        half_t* patches, int Kp, int slots, hipStream_t s);
 void launch_im2col_f16(const half_t* act, int batch, int C, int H, int W, half_t* patches, int Kp, hipStream_t s);
 void launch_tokens(const half_t* stem_out, int n_spatial, int C5, half_t* F, hipStream_t s);
+
+// ---- content hash of device tensors (hash.hip) --------------------------------
+constexpr int HASH_SPAN_BYTES = 64 << 10;
+struct HashSpan {
+  const uint8_t* p;   // tensor base
+  long off;           // span start, bytes (a multiple of 16)
+  int n;              // span length, bytes (<= HASH_SPAN_BYTES)
+  int tensor;         // index of the tensor the span belongs to (host bookkeeping)
+};
+__host__ __device__ uint64_t hash_mix(uint64_t z);
+// partial[i] = the sum over span i's chunks; a tensor's hash is hash_mix(n)
+// plus the sum of its spans' partials (mod 2^64).
+void launch_state_hash(const HashSpan* spans, int n_spans, unsigned long long* partial, hipStream_t s);
 
 // ---- KATs --------------------------------------------------------------------
 // RDNA4 wave32 WMMA fragments (u16 [32][8] A, B; f32 [32][8] C) -> D fragment,

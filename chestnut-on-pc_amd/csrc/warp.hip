@@ -12,9 +12,15 @@
 // channel planes: the four Y pixels (2i+{0,1}, 2j+{0,1}) -> channels 0..3
 // (even/odd rows x even/odd columns) and U, V at (i, j) -> channels 4, 5.
 //
-// The coordinate arithmetic is f32 operation by operation with
-// contraction off -- (M00*x + M01*y) + M02, then an IEEE division -- so the
-// sampled texel is the one the reference's f32 graph selects, bit for bit.
+// The coordinate arithmetic is f32 operation by operation with contraction
+// off -- (M00*x + M01*y) + M02, then the division -- and the texel is the one
+// that f32 arithmetic, evaluated in that order, selects.  The reference
+// writes the division as src_x / src_w (compile_modeld.py:65-66); what that
+// rounds to depends on how its graph is lowered (the reference's own engine
+// rewrites every f32 division as x * rcp(y), run_pinned2.py:622-628), and
+// the two forms pick different texels at a few .5 boundaries per frame.
+// `rcp` selects the form: 0 the correctly rounded quotient, 1 the product
+// with the correctly rounded reciprocal.
 #include "common.h"
 #include "kernels.h"
 
@@ -22,17 +28,28 @@ namespace ck {
 namespace {
 
 #pragma clang fp contract(off)
+template <bool RCP>
 __device__ __forceinline__ void warp_coord(const float* __restrict__ M, float x, float y, int w_src, int h_src, int& xc,
                                            int& yc) {
   const float sx = (M[0] * x + M[1] * y) + M[2];
   const float sy = (M[3] * x + M[4] * y) + M[5];
   const float sw = (M[6] * x + M[7] * y) + M[8];
-  const float xr = rintf(sx / sw), yr = rintf(sy / sw);
+  float qx, qy;
+  if (RCP) {
+    const float r = 1.0f / sw;   // correctly rounded (no fast-math reciprocal)
+    qx = sx * r;
+    qy = sy * r;
+  } else {
+    qx = sx / sw;
+    qy = sy / sw;
+  }
+  const float xr = rintf(qx), yr = rintf(qy);
   xc = (int)fminf(fmaxf(xr, 0.f), (float)(w_src - 1));
   yc = (int)fminf(fmaxf(yr, 0.f), (float)(h_src - 1));
 }
 #pragma clang fp contract(on)
 
+template <bool RCP>
 __global__ __launch_bounds__(256) void warp_nv12_kernel(const uint8_t* __restrict__ f0, const uint8_t* __restrict__ f1,
                                                         const float* __restrict__ m0, const float* __restrict__ m1,
                                                         int cam_w, int cam_h, int stride, long uv_offset, int W, int H,
@@ -58,11 +75,11 @@ __global__ __launch_bounds__(256) void warp_nv12_kernel(const uint8_t* __restric
   for (int c = 0; c < 4; ++c) {
     const int yy = 2 * i + (c & 1), xx = 2 * j + (c >> 1);
     int xc, yc;
-    warp_coord(M, (float)xx, (float)yy, cam_w, cam_h, xc, yc);
+    warp_coord<RCP>(M, (float)xx, (float)yy, cam_w, cam_h, xc, yc);
     o[(long)c * n] = src[(long)yc * stride + xc];
   }
   int xc, yc;
-  warp_coord(Mu, (float)j, (float)i, cam_w / 2, cam_h / 2, xc, yc);
+  warp_coord<RCP>(Mu, (float)j, (float)i, cam_w / 2, cam_h / 2, xc, yc);
   const uint8_t* uv = src + uv_offset + (long)yc * stride + 2 * xc;
   o[4 * n] = uv[0];
   o[5 * n] = uv[1];
@@ -72,8 +89,9 @@ __global__ __launch_bounds__(256) void warp_nv12_kernel(const uint8_t* __restric
 
 void launch_warp_nv12(const uint8_t* frame, const uint8_t* big_frame, size_t frame_bytes, const float* tfm,
                       const float* big_tfm, int cam_w, int cam_h, int stride, int y_height, int model_w, int model_h,
-                      uint8_t* out, hipStream_t s) {
+                      int division, uint8_t* out, hipStream_t s) {
   CK_REQUIRE(frame && big_frame && tfm && big_tfm && out, "warp_nv12: null pointer");
+  CK_REQUIRE(division == 0 || division == 1, "warp_nv12: division must be 0 (quotient) or 1 (reciprocal product)");
   CK_REQUIRE(cam_w > 0 && cam_h > 0 && cam_w % 2 == 0 && cam_h % 2 == 0, "warp_nv12: camera size must be even");
   CK_REQUIRE(stride >= cam_w && y_height >= cam_h, "warp_nv12: stride >= width and y_height >= height required");
   CK_REQUIRE(model_w > 0 && model_h > 0 && model_w % 4 == 0 && model_h % 4 == 0,
@@ -82,8 +100,12 @@ void launch_warp_nv12(const uint8_t* frame, const uint8_t* big_frame, size_t fra
   CK_REQUIRE((size_t)(uv_offset + (long)(cam_h / 2) * stride) <= frame_bytes,
              "warp_nv12: frame buffer smaller than its Y plane and the UV rows the warp reads");
   const long n = 2L * (model_h / 2) * (model_w / 2);
-  CK_LAUNCH(warp_nv12_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, frame, big_frame, tfm,
-                     big_tfm, cam_w, cam_h, stride, uv_offset, model_w, model_h, out);
+  if (division)
+    CK_LAUNCH(warp_nv12_kernel<true>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, frame, big_frame, tfm,
+              big_tfm, cam_w, cam_h, stride, uv_offset, model_w, model_h, out);
+  else
+    CK_LAUNCH(warp_nv12_kernel<false>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, frame, big_frame, tfm,
+              big_tfm, cam_w, cam_h, stride, uv_offset, model_w, model_h, out);
   CK_LAUNCHED("warp_nv12");
 }
 

@@ -151,6 +151,16 @@ int ck_tensor(ck_engine* e, const char* name, void** dptr, size_t* nbytes);
  * Replaces: the probes' per-argument span discovery (r62_probe.py:31-35). */
 int ck_state_count(ck_engine* e, int* n);
 int ck_state_info(ck_engine* e, int i, char* name, size_t name_len, size_t* nbytes, int* dtype);
+/* A 64-bit content hash of every state tensor (ck_state_info order, whole
+ * tensor, computed on the device after the work queued on the engine
+ * stream; synchronises).  Taken before each launch of an eager frame it is
+ * the launch's pre-state fingerprint; two runs' fingerprints name the first
+ * launch after which they diverge, and which tensors differ.  n >= the
+ * state count.
+ * Replaces: KSYNC's md5 of each launch's argument pre-state
+ * (run_pinned2.py:1519-1542) and research/xcheck.py's per-argument hashes
+ * (research/xcheck.py:65-124). */
+int ck_state_hashes(ck_engine* e, uint64_t* out, int n);
 int ck_read_tensor(ck_engine* e, const char* name, void* host, size_t nbytes);
 int ck_write_tensor(ck_engine* e, const char* name, const void* host, size_t nbytes);
 
@@ -205,11 +215,16 @@ int ck_gemm_epi(const void* A, const void* B, void* C, const float* bias, int M,
  * frame, big_frame: device NV12 buffers of frame_bytes (Y plane: y_height
  * rows of stride bytes, then the UV plane); tfm, big_tfm: device f32 [3][3]
  * inverse transforms; out: device u8 [2][6][model_h/2][model_w/2].
+ * division: how src_x / src_w is evaluated -- 0 the correctly rounded f32
+ * quotient, 1 the product with the correctly rounded f32 reciprocal (the
+ * reference writes the quotient, compile_modeld.py:65-66, and its engine
+ * lowers f32 divisions to x * rcp(y), run_pinned2.py:622-628; the forms
+ * pick different texels at a few .5 boundaries per frame).
  * Replaces: make_warp / frame_prepare_tinygrad / warp_perspective_tinygrad
  * (compile_modeld.py:53-118, 181-193). */
 int ck_warp_nv12(const uint8_t* frame, const uint8_t* big_frame, size_t frame_bytes, const float* tfm,
                  const float* big_tfm, int cam_w, int cam_h, int stride, int y_height, int model_w, int model_h,
-                 uint8_t* out, void* stream);
+                 int division, uint8_t* out, void* stream);
 
 /* n_tiles WMMA uops ((16,16,16), half, 'AMD', 32): per tile u16 fragA[32][8],
  * fragB[32][8], f32 fragC[32][8] -> f32 fragD[32][8], RDNA4 lane layout.

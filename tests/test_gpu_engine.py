@@ -292,12 +292,14 @@ def test_1b_frames_vs_oracle(gpu):
             hs = out[eng.out_slices['hidden_state']]
 
 
-def test_nv12_frames_vs_oracle(gpu):
+@pytest.mark.parametrize('division', ['ieee', 'rcp'])
+def test_nv12_frames_vs_oracle(gpu, division):
     """modeld's flow: NV12 frames + transforms -> device warp -> frame.  The
-    warped input matches the oracle warp bit for bit and the outputs match
-    the oracle model run on the oracle-warped frames."""
+    warped input matches the oracle warp bit for bit (in the division form
+    the spec's camera selects) and the outputs match the oracle model run on
+    the oracle-warped frames."""
     from oracle import warp as OW
-    cam = dict(width=320, height=200, stride=384, y_height=208)
+    cam = dict(width=320, height=200, stride=384, y_height=208, division=division)
     sp = dict(S.get_spec('tiny'), camera=cam)
     w = S.make_weights(sp)
     nb = S.nv12_bytes(cam)
@@ -318,7 +320,7 @@ def test_nv12_frames_vs_oracle(gpu):
                 packed[12:] = pk_dev
             print(f'[nv12] frame {f}', flush=True)
             out = eng.run_frame_nv12(frame, big, tfm, big_tfm, packed)
-            warped = OW.warp(tfm, big_tfm, frame, big, nv12, 2 * sp['img_w'], 2 * sp['img_h'])
+            warped = OW.warp(tfm, big_tfm, frame, big, nv12, 2 * sp['img_w'], 2 * sp['img_h'], div=division)
             np.testing.assert_array_equal(eng.read('warped', np.uint8, warped.shape), warped)
             ref = orc.run_frame(warped, packed)
             for name, sl in eng.out_slices.items():

@@ -27,18 +27,45 @@ def _tfms(rng):
     return [(persp, far), (half, np.eye(3, dtype=np.float32))]
 
 
-def test_warp_nv12_bit_exact(gpu):
+@pytest.mark.parametrize('division', OW.DIVISIONS)
+def test_warp_nv12_bit_exact(gpu, division):
     from chestnut import kernels as K
     torch = gpu
     rng = np.random.default_rng(7)
     frame, big = _frame(rng), _frame(rng)
     nv12 = (CAM['cam_w'], CAM['cam_h'], CAM['stride'], CAM['y_height'], CAM['cam_h'] // 2)
     for tfm, big_tfm in _tfms(rng):
-        print(f'[warp] tfm {tfm.ravel()[:3]} big {big_tfm.ravel()[:3]}', flush=True)
+        print(f'[warp] {division} tfm {tfm.ravel()[:3]} big {big_tfm.ravel()[:3]}', flush=True)
         got = K.warp_nv12(torch.from_numpy(frame).cuda(), torch.from_numpy(big).cuda(),
-                          torch.from_numpy(tfm).cuda(), torch.from_numpy(big_tfm).cuda(), **CAM).cpu().numpy()
-        ref = OW.warp(tfm, big_tfm, frame, big, nv12, 512, 256)
+                          torch.from_numpy(tfm).cuda(), torch.from_numpy(big_tfm).cuda(), **CAM,
+                          division=division).cpu().numpy()
+        ref = OW.warp(tfm, big_tfm, frame, big, nv12, 512, 256, div=division)
         np.testing.assert_array_equal(got, ref)
+
+
+def test_warp_nv12_division_forms(gpu):
+    """Over seeded road-camera transforms the two division forms pick
+    different texels at a few pixels; the device matches the oracle's form
+    bit for bit in both, so the switch selects exactly the stated arithmetic."""
+    from chestnut import kernels as K
+    torch = gpu
+    rng = np.random.default_rng(8)
+    frame, big = _frame(rng), _frame(rng)
+    nv12 = (CAM['cam_w'], CAM['cam_h'], CAM['stride'], CAM['y_height'], CAM['cam_h'] // 2)
+    base = np.array([[3.7, -0.05, 10.0], [0.05, 3.7, 120.0], [1e-5, 2e-5, 1.0]], np.float32)
+    differ = 0
+    for t in range(4):
+        tfm = (base * (1 + 0.02 * rng.standard_normal((3, 3)))).astype(np.float32)
+        big_tfm = (base * (1 + 0.02 * rng.standard_normal((3, 3)))).astype(np.float32)
+        print(f'[warp] forms transform {t}', flush=True)
+        got = {}
+        for div in OW.DIVISIONS:
+            got[div] = K.warp_nv12(torch.from_numpy(frame).cuda(), torch.from_numpy(big).cuda(),
+                                   torch.from_numpy(tfm).cuda(), torch.from_numpy(big_tfm).cuda(), **CAM,
+                                   division=div).cpu().numpy()
+            np.testing.assert_array_equal(got[div], OW.warp(tfm, big_tfm, frame, big, nv12, 512, 256, div=div))
+        differ += int((got['ieee'] != got['rcp']).sum())
+    assert differ > 0
 
 
 def test_warp_nv12_rejects_short_buffer(gpu):
@@ -54,4 +81,4 @@ def test_warp_nv12_rejects_short_buffer(gpu):
     p = lambda t: ctypes.c_void_p(t.data_ptr())              # noqa: E731
     with pytest.raises(RuntimeError, match='frame buffer smaller'):   # the native entry point's own check
         call('ck_warp_nv12', p(f), p(f), f.numel(), p(m), p(m), CAM['cam_w'], CAM['cam_h'], CAM['stride'],
-             CAM['y_height'], 512, 256, p(out), None)
+             CAM['y_height'], 512, 256, 0, p(out), None)

@@ -43,6 +43,22 @@ def test_gemv_gelu_closed_form():
     assert abs(g[3] - 3.0 * 0.5 * (1 + np.tanh(np.sqrt(2 / np.pi) * (3 + 0.044715 * 27)))) < 1e-12
 
 
+def test_gelu_published_values_and_library():
+    """The tanh form against values published for it (Hendrycks & Gimpel's
+    approximation: gelu(1) = 0.841192, gelu(-1) = -0.158808, gelu(2) =
+    1.954598) and against torch's own tanh-approximate GELU in float64; the
+    erf form differs at x = 1 by 1.5e-4, so an erf GELU, a dropped cubic term
+    or a wrong constant fails here."""
+    import torch
+    x = np.array([1.0, -1.0, 2.0])
+    np.testing.assert_allclose(K.gelu(x), [0.841192, -0.158808, 1.954598], atol=1e-6)
+    from math import erf, sqrt
+    assert abs(K.gelu(np.array([1.0]))[0] - 0.5 * (1 + erf(1 / sqrt(2)))) > 1e-4
+    grid = np.linspace(-8, 8, 4001)
+    ref = torch.nn.functional.gelu(torch.from_numpy(grid), approximate='tanh').numpy()
+    np.testing.assert_allclose(K.gelu(grid), ref, rtol=0, atol=1e-14)
+
+
 def test_gemm_bruteforce_and_layouts():
     rng = np.random.default_rng(2)
     A = rng.standard_normal((4, 4)).astype(np.float16)

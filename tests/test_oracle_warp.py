@@ -70,3 +70,57 @@ def test_frame_prepare_identity_equals_frames_to_tensor():
     i420 = np.concatenate([Y.reshape(-1), UV[:, 0:w:2].reshape(-1), UV[:, 1:w:2].reshape(-1)]).reshape(h * 3 // 2, w)
     np.testing.assert_array_equal(out, OP.frames_to_tensor(i420))
     assert out.shape == (6, h // 2, w // 2)
+
+
+def _road_tfms(n, seed=0):
+    """Seeded perturbations of a road-camera transform (model pixel ->
+    camera pixel: scale about 3.7, offset into the frame, slight perspective)."""
+    base = np.array([[3.7, -0.05, 10.0], [0.05, 3.7, 120.0], [1e-5, 2e-5, 1.0]], np.float32)
+    rng = np.random.default_rng(seed)
+    return [(base * (1 + 0.02 * rng.standard_normal((3, 3)))).astype(np.float32) for _ in range(n)]
+
+
+def test_division_forms_differ_by_at_most_one_texel():
+    """The reference writes src_x / src_w (compile_modeld.py:65-66); its engine
+    lowers f32 divisions to x * rcp(y) (run_pinned2.py:622-628).  Counted over
+    the Y and UV planes of 8 road-camera warps (1928x1208 -> 512x256): the two
+    forms pick different texels at a handful of pixels per plane (35 of
+    1,310,720 here), never more than one texel apart, and agree exactly
+    wherever the transform is affine (src_w = 1)."""
+    diff, total = 0, 0
+    for M in _road_tfms(8):
+        for Mx, dst in ((M, (512, 256)), ((M * W.UV_SCALE).astype(np.float32), (256, 128))):
+            xi, yi = W.warp_rounded(Mx, dst, 'ieee')
+            xr, yr = W.warp_rounded(Mx, dst, 'rcp')
+            d = (xi != xr) | (yi != yr)
+            diff += int(d.sum())
+            total += d.size
+            assert np.abs(xi - xr).max() <= 1 and np.abs(yi - yr).max() <= 1
+    assert 0 < diff < 1e-4 * total, diff
+    assert diff == 35
+    affine = np.array([[3.7, -0.05, 10.25], [0.05, 3.7, 120.5], [0.0, 0.0, 1.0]], np.float32)
+    for div in W.DIVISIONS:
+        assert all(np.array_equal(a, b) for a, b in zip(W.warp_rounded(affine, (512, 256), 'ieee'),
+                                                        W.warp_rounded(affine, (512, 256), div)))
+
+
+def test_rcp_form_by_hand():
+    """src_x * (1 / src_w) evaluated as two correctly rounded f32 operations:
+    a case where it differs from the quotient, checked with exact rationals."""
+    from fractions import Fraction as Fr
+    F = np.float32
+    # scan a small range for a pair whose two f32 forms disagree, then check both against exact arithmetic
+    for sx_i in range(1, 4000):
+        sx, sw = F(sx_i * 0.37), F(3.0)
+        q, r = F(sx / sw), F(sx * F(F(1.0) / sw))
+        if q != r:
+            break
+    else:
+        raise AssertionError('no differing pair found')
+    exact_q = Fr(float(sx)) / Fr(float(sw))
+    exact_r = Fr(float(sx)) * Fr(float(F(F(1.0) / sw)))
+    # each form is the f32 nearest its exact value
+    for got, ex in ((q, exact_q), (r, exact_r)):
+        nb = [np.nextafter(got, F(-np.inf)), got, np.nextafter(got, F(np.inf))]
+        errs = [abs(Fr(float(v)) - ex) for v in nb]
+        assert errs[1] == min(errs)
