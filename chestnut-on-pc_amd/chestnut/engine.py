@@ -280,6 +280,35 @@ class Engine:
         for n, a in state.items():
             self.write(n, a)
 
+    def state_hashes(self):
+        """{name: 64-bit content hash} of every state tensor, whole tensor,
+        computed on the device after the work already queued (ck_state_hashes)."""
+        names = [n for n, _, _ in self.state_names()]
+        out = (ctypes.c_uint64 * len(names))()
+        call('ck_state_hashes', self._h, out, len(names))
+        return dict(zip(names, (int(v) for v in out)))
+
+    def fingerprints(self, frames=1, timed=True):
+        """KSYNC with pre-state fingerprints (run_pinned2.py:1513-1557): `frames`
+        eager frames launch by launch, each launch's pre-state hashed (every
+        state tensor, ck_state_hashes) and, with `timed`, the launch timed
+        alone between HIP events.  Returns a list with one row per launch,
+        {'frame', 'index', 'name', 'kernel', 'ms', 'pre': {tensor: hash}},
+        plus a last row (index = plan size) holding the state after the final
+        launch.  The frames continue the engine's recurrent state."""
+        plan = self.plan()
+        rows = []
+        for f in range(frames):
+            for i, e in enumerate(plan):
+                pre = self.state_hashes()
+                ms = self.time_launches([i], 1) if timed else None
+                if not timed:
+                    self.run_range(i, i + 1)
+                rows.append({'frame': f, 'index': i, 'name': e['name'], 'kernel': e['kernel'], 'ms': ms, 'pre': pre})
+        rows.append({'frame': frames - 1, 'index': len(plan), 'name': '(end of frame)', 'kernel': '', 'ms': None,
+                     'pre': self.state_hashes()})
+        return rows
+
 
 class Queues(Mapping):
     """The reference's `queues` dict (run_pinned2.py:1379-1386), read live

@@ -21,13 +21,28 @@ baseline's (bench_r62.py:25-65).  Here:
             argument) -- restore the captured pre-state, time the entry the
             same way and compare every state tensor with post.npz.
 
+  fingerprint  run `warm` frames of make_warped(val) through the graph or
+            plain launches, then `frames` eager frames launch by launch: each
+            launch's pre-state fingerprint (a device hash of every state
+            tensor, ck_state_hashes) and its time, printed as KSYNC prints
+            them (run_pinned2.py:1519-1550) and written to a JSON file.
+
+  diff      two fingerprint files (graph against eager warm frames, one
+            build against another, one spec option against another): the
+            first launch after which the states differ, and the tensors that
+            differ there -- xcheck's launch-by-launch comparison of two runs
+            (research/xcheck.py:65-124, 150-200).
+
     python -m chestnut.probe capture --spec big_driving_1b --entry blk0.up --out DIR
     python -m chestnut.probe bench DIR [--lib PATH] [--gemm 5,2] [--reps 15] [--ignore ws]
+    python -m chestnut.probe fingerprint --spec tiny [--warm 3 --warm-mode graph] [--lib PATH] --out A.json
+    python -m chestnut.probe diff A.json B.json [--ignore ws]
 
 Timings are per launch (HIP events around the single entry, no host
 launch overhead), so `med` is the kernel's own duration.
 """
 import argparse
+import hashlib
 import json
 import os
 import sys
@@ -163,6 +178,67 @@ def bench(d, lib=None, gemm=None, reps=None, ignore=()):
     return res
 
 
+def state_digest(pre, ignore=()):
+    """8 hex digits over a launch's whole pre-state (KSYNC's pre=...)."""
+    h = hashlib.md5()
+    for name in sorted(pre):
+        if name not in ignore:
+            h.update(f'{name}:{pre[name]:016x};'.encode())
+    return h.hexdigest()[:8]
+
+
+def fingerprint(spec, out=None, frames=1, warm=0, warm_mode='graph', val=111, lib=None, extra=None, log=print):
+    """Fingerprinted eager frames after `warm` frames in `warm_mode`; returns
+    (and writes to `out`) {'meta': ..., 'rows': Engine.fingerprints rows}."""
+    from . import spec as S
+    sp = dict(S.get_spec(spec), **(extra or {}))
+    eng = _engine(sp, lib)
+    try:
+        warped = eng.make_warped(val)
+        packed = eng.PACKED.copy()
+        packed[8:10] = (1.0, 0.0)
+        eng.set_graph(warm_mode == 'graph')
+        for _ in range(warm):
+            o = eng.run_frame(warped, packed)
+            packed[12:] = o[eng.out_slices['hidden_state']]
+        eng.write('warped', warped)
+        eng.write('packed', packed)
+        rows = eng.fingerprints(frames)
+    finally:
+        eng.close()
+    for r in rows:
+        ms = f"{r['ms']:7.3f}ms" if r['ms'] is not None else ' ' * 9
+        log(f"[ksync] {r['frame']}:{r['index']:3d} {r['name']:32} {ms} pre={state_digest(r['pre'])}")
+    tot = sum(r['ms'] for r in rows if r['ms'] is not None)
+    log(f'[ksync] total kernel GPU time = {tot:.2f}ms over {sum(r["ms"] is not None for r in rows)} launches')
+    res = {'meta': {'spec': sp['name'], 'frames': frames, 'warm': warm, 'warm_mode': warm_mode, 'val': val,
+                    'lib': lib}, 'rows': [dict(r, pre={k: f'{v:016x}' for k, v in r['pre'].items()}) for r in rows]}
+    if out:
+        os.makedirs(os.path.dirname(os.path.abspath(out)), exist_ok=True)
+        with open(out, 'w') as fh:
+            json.dump(res, fh)
+    return res
+
+
+def diff(a, b, ignore=()):
+    """First divergence of two fingerprint runs: rows are matched by (frame,
+    index); at the first row whose pre-states differ, the launch before it
+    (the previous row) is the first one whose results differ -- or, at row 0,
+    the runs already differed before the fingerprinted frames.  Returns None
+    when every pre-state agrees."""
+    ra, rb = a['rows'], b['rows']
+    if [(r['frame'], r['index'], r['name']) for r in ra] != [(r['frame'], r['index'], r['name']) for r in rb]:
+        raise ValueError('the two runs have different plans or frame counts')
+    for k, (x, y) in enumerate(zip(ra, rb)):
+        dt = sorted(n for n in x['pre'] if n not in ignore and x['pre'][n] != y['pre'].get(n))
+        if dt:
+            prev = ra[k - 1] if k else None
+            return {'row': k, 'before': x['name'], 'frame': x['frame'], 'index': x['index'],
+                    'launch': (prev['name'] if prev else None), 'launch_index': (prev['index'] if prev else None),
+                    'tensors': dt}
+    return None
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(prog='python -m chestnut.probe', description=__doc__.split('\n\n')[0])
     sub = ap.add_subparsers(dest='cmd', required=True)
@@ -180,7 +256,37 @@ def main(argv=None):
     b.add_argument('--gemm', default=None, help='TILE,SPLIT for the entry in the variant')
     b.add_argument('--reps', type=int, default=None)
     b.add_argument('--ignore', default='', help='comma-separated scratch tensors left out of the totals (e.g. ws)')
+    f = sub.add_parser('fingerprint')
+    f.add_argument('--spec', default='big_driving_1b')
+    f.add_argument('--out', required=True)
+    f.add_argument('--frames', type=int, default=1)
+    f.add_argument('--warm', type=int, default=0, help='frames run before the fingerprinted ones')
+    f.add_argument('--warm-mode', choices=('graph', 'eager'), default='graph')
+    f.add_argument('--val', type=int, default=111)
+    f.add_argument('--lib', default=None)
+    f.add_argument('--set', default=None, help='JSON object of spec options, e.g. {"fuse_head": 0}')
+    d = sub.add_parser('diff')
+    d.add_argument('a')
+    d.add_argument('b')
+    d.add_argument('--ignore', default='', help='comma-separated tensors left out (e.g. ws)')
     a = ap.parse_args(argv)
+    if a.cmd == 'fingerprint':
+        fingerprint(a.spec, a.out, a.frames, a.warm, a.warm_mode, a.val, a.lib,
+                    json.loads(a.set) if a.set else None)
+        return 0
+    if a.cmd == 'diff':
+        with open(a.a) as fa, open(a.b) as fb:
+            r = diff(json.load(fa), json.load(fb), tuple(x for x in a.ignore.split(',') if x))
+        if r is None:
+            print('[diff] identical: every launch of both runs saw the same pre-state', flush=True)
+            return 0
+        if r['launch'] is None:
+            print(f"[diff] the runs differ before the first fingerprinted launch ({r['before']}): "
+                  f"{', '.join(r['tensors'])}", flush=True)
+        else:
+            print(f"[diff] first divergent launch: frame {r['frame']} #{r['launch_index']} {r['launch']} "
+                  f"-> differs in {', '.join(r['tensors'])}", flush=True)
+        return 1
     gemm = tuple(int(x) for x in a.gemm.split(',')) if a.gemm else None
     if a.cmd == 'capture':
         m = capture(a.spec, a.entry, a.out, a.frames, a.val, a.reps, gemm)
