@@ -241,20 +241,106 @@ def traffic_record(spec_name, fam):
     return None
 
 
+def cpu_cores():
+    """Threads for the CPU baseline: every core of the process's affinity
+    mask, capped by the CPU share the host grants one GPU's job when it
+    states one (OMP_NUM_THREADS, 16 on the GPU boxes)."""
+    affinity = len(os.sched_getaffinity(0))
+    share = int(os.environ.get('OMP_NUM_THREADS', '0') or 0)
+    return (min(affinity, share) if share > 0 else affinity), affinity
+
+
+def _median_s(fn, reps):
+    fn()                                         # warm-up (first touch, BLAS thread start)
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return float(np.median(ts)), ts
+
+
+def cpu_configs(weights_1b, sp_1b, gpu, reps=5):
+    """BASELINE configs 1-4 through the oracle on this host's cores, each
+    beside the GPU figure of the same run (`gpu`: config -> (value, unit)).
+    Medians of `reps` timed repetitions after one untimed one.
+
+      1  GEMM A f16 [1024, 6144] . B f16 [6144, 1024] -> f32: numpy f32
+         (OpenBLAS sgemm, operands converted outside the timed region), and
+         oracle.kernels.gemm_kchain16, the reference's K-chained FFMA order
+         (one sequential f32 multiply-add per k, run_pinned2.py:183-191),
+         single-threaded numpy, timed on the first 512 of the 6144 k and
+         scaled by 12 (its cost is linear in K);
+      2  GEMV W f16 [3072, 12288] . x f32: numpy f32 (OpenBLAS sgemv, W
+         converted outside the timed region);
+      3  one pre-LN block (block 0 of the 1B model's weights, x ~ N(0, 1)):
+         oracle.model.block_forward in f32;
+      4  the 39M analogue's recurrent frame: oracle.model.OracleModel in f32.
+    """
+    from threadpoolctl import threadpool_limits
+    from oracle import kernels as OK
+    from oracle.model import OracleModel, block_forward
+    from chestnut import spec as S
+    cores, _ = cpu_cores()
+    out = {}
+    with threadpool_limits(limits=cores):
+        rng = np.random.default_rng(1)
+        A = (rng.standard_normal((1024, 6144)) / np.sqrt(6144)).astype(np.float16)
+        B = (rng.standard_normal((6144, 1024)) / np.sqrt(6144)).astype(np.float16)
+        A32, B32 = A.astype(np.float32), B.astype(np.float32)
+        med, ts = _median_s(lambda: A32 @ B32, reps)
+        out['config1'] = {'value': round(med * 1e6, 1), 'unit': 'us per GEMM', 'cores': cores, 'kind': 'port',
+                          'sample': f'numpy f32 (OpenBLAS sgemm) 1024x6144 @ 6144x1024, median of {reps}'}
+        kc = 512
+        with threadpool_limits(limits=1):
+            med_k, _ = _median_s(lambda: OK.gemm_kchain16(A[:, :kc], B[:kc]), max(2, reps // 2))
+        out['config1_kchain16'] = {'value': round(med_k * (6144 / kc) * 1e6, 1), 'unit': 'us per GEMM',
+                                   'cores': 1, 'kind': 'port',
+                                   'sample': f'oracle.kernels.gemm_kchain16 (sequential f32 FFMA chain over k) '
+                                             f'on the first {kc} of 6144 k, median of {max(2, reps // 2)}, '
+                                             f'scaled by {6144 // kc}'}
+        del A, B, A32, B32
+        W32 = (rng.standard_normal((3072, 12288)) * 0.02).astype(np.float16).astype(np.float32)
+        x = rng.uniform(-1, 1, 12288).astype(np.float32)
+        med, _ = _median_s(lambda: W32 @ x, reps)
+        out['config2'] = {'value': round(med * 1e6, 1), 'unit': 'us per GEMV', 'cores': cores, 'kind': 'port',
+                          'sample': f'numpy f32 (OpenBLAS sgemv) [3072, 12288] . [12288], median of {reps}'}
+        del W32
+        xb = rng.standard_normal((512, 2048)).astype(np.float32)
+        med, _ = _median_s(lambda: block_forward(xb, weights_1b, 0, sp_1b, acc=np.float32), reps)
+        out['config3'] = {'value': round(med * 1e6, 1), 'unit': 'us per block', 'cores': cores, 'kind': 'port',
+                          'sample': f'oracle.model.block_forward (f32, weights converted per call) d=2048 T=512, '
+                                    f'median of {reps}'}
+        sp4 = S.get_spec('driving_39m')
+        orc = OracleModel(sp4, S.make_weights(sp4), acc=np.float32)
+        warped = rng.integers(0, 256, (2, 6, sp4['img_h'], sp4['img_w']), dtype=np.uint8)
+        pk = np.zeros(sp4['desire_len'] + 4 + sp4['feat_len'], np.float32)
+        pk[8:10] = (1.0, 0.0)
+
+        def frame():
+            o = orc.run_frame(warped, pk)
+            pk[12:] = o[-sp4['hidden']:]
+        med, _ = _median_s(frame, reps)
+        out['config4'] = {'value': round(1.0 / med, 2), 'unit': 'frames/s', 'cores': cores, 'kind': 'port',
+                          'sample': f'driving_39m through oracle/model.py (f32), recurrent frames, median of {reps}'}
+    for k, v in out.items():
+        g = gpu.get(k.split('_')[0])
+        if g:
+            v['gpu'] = {'value': g[0], 'unit': g[1]}
+            v['gpu_over_cpu'] = round(v['value'] / g[0] if 'us' in v['unit'] else g[0] / v['value'], 1)
+    return out
+
+
 def cpu_baseline(sp, weights, warped, packed, reps=5):
     """The numpy oracle (f32 OpenBLAS) on this host's cores, bounded sample:
     one warm-up frame, then `reps` timed frames (the recurrent loop, hidden
     state fed back), reported as the median frame rate.
 
-    Threads: every core of the process's affinity mask, capped by the CPU
-    share the host grants one GPU's job when it states one (OMP_NUM_THREADS,
-    16 on the GPU boxes), exported as OPENBLAS_NUM_THREADS and applied to the
+    Threads: cpu_cores(), exported as OPENBLAS_NUM_THREADS and applied to the
     loaded BLAS with threadpoolctl."""
     from threadpoolctl import threadpool_info, threadpool_limits
     from oracle.model import OracleModel
-    affinity = len(os.sched_getaffinity(0))
-    share = int(os.environ.get('OMP_NUM_THREADS', '0') or 0)
-    cores = min(affinity, share) if share > 0 else affinity
+    cores, affinity = cpu_cores()
     os.environ['OPENBLAS_NUM_THREADS'] = str(cores)
     with threadpool_limits(limits=cores):
         blas = [f"{i.get('internal_api')}x{i.get('num_threads')}" for i in threadpool_info()
@@ -453,6 +539,16 @@ def main():
     if not a.no_cpu:
         line['cpu_baseline'] = cpu_baseline(sp, weights, warped, packed, a.cpu_reps)
         log(f'[bench] cpu baseline {line["cpu_baseline"]}')
+        gpu = {}
+        if 'micro' in line:
+            gpu['config1'] = (line['micro']['gemm_config1']['us'], 'us per GEMM')
+            gpu['config2'] = (line['micro']['gemv_config2']['us'], 'us per GEMV')
+        if c3:
+            gpu['config3'] = (c3['us_per_block'], 'us per block')
+        if 'config4' in line:
+            gpu['config4'] = (line['config4']['graph_fps'], 'frames/s')
+        line['cpu_baseline']['configs'] = cpu_configs(weights, sp, gpu, a.cpu_reps)
+        log(f'[bench] cpu configs {line["cpu_baseline"]["configs"]}')
     print(json.dumps(line), flush=True)
 
 

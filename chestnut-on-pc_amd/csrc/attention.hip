@@ -319,6 +319,8 @@ void launch_attention(const half_t* qk, const half_t* vt, half_t* out, int T, in
   CK_REQUIRE(T > 0 && T % 64 == 0 && T <= ATT_TMAX, "attention: T must be a multiple of 64 and <= 512");
   CK_REQUIRE(head_dim == 64 || head_dim == 128, "attention: head_dim must be 64 or 128");
   CK_REQUIRE(n_heads > 0, "attention: n_heads must be positive");
+  // the output leaves through raw buffer stores addressed by 32-bit offsets
+  CK_REQUIRE(2L * T * n_heads * head_dim < (1L << 31), "attention: output must be under 2 GiB");
   CK_REQUIRE((reinterpret_cast<uintptr_t>(qk) & 15) == 0 && (reinterpret_cast<uintptr_t>(vt) & 15) == 0 &&
                  (reinterpret_cast<uintptr_t>(out) & 7) == 0,
              "attention: qk and vt must be 16-byte and out 8-byte aligned");

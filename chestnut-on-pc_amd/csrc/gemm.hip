@@ -396,11 +396,13 @@ __device__ __forceinline__ void dma_issue(const half_t* const* asrc, const half_
 // columns are staged transposed ([n][m]), four consecutive rows of a lane
 // forming one 8-byte LDS write, so V^T rows leave contiguously as well.
 // Row pitches carry 16 bytes of padding so the two half-waves' staging
-// writes (rows r and r+4) fall in different banks.  The split-K partials,
-// the row-major f16 outputs and the QKV fragments, read by the next kernel,
-// leave with the device-scope cache policy (store_sc1: -0.5%, -0.4% and
-// -0.3% of the 1B frame against non-temporal or default stores); the f32
-// outputs with non-temporal stores.
+// writes (rows r and r+4) fall in different banks.  Every staged output --
+// split-K partials, f32 outputs (plain, residual-add, embedding), row-major
+// f16 outputs and the QKV fragments, all read by the next kernel -- leaves
+// with the device-scope cache policy (store_sc1: -0.5%, -0.4% and -0.3% of
+// the 1B frame for the partials, the f16 outputs and the fragments against
+// non-temporal or default stores) wherever the region is addressable by a
+// 32-bit buffer offset (sc1_ok), and with non-temporal stores otherwise.
 // Requires (checked on the host, else the direct per-element stores run):
 // N % 8 == 0, ldc / batch stride / base of C and ws 16-byte compatible,
 // and for QKV qk_cols % BN == 0, M % 8 == 0 and vt_ld % 8 == 0.
@@ -1217,6 +1219,9 @@ void launch_gemm(GemmDesc d, hipStream_t s) {
                "than a wave's columns, M % 32 == 0");
     CK_REQUIRE(d.split == 1 && d.batch == 1 && tile_dma(d.tile) && p.vec,
                "gemm: QKV fragment epilogue needs split 1, batch 1, an LDS-DMA tile and aligned outputs");
+    // Q/K and V fragments leave through raw buffer stores addressed by 32-bit offsets
+    CK_REQUIRE(2L * d.M * d.qk_cols < (1L << 31) && 2L * d.M * (d.N - d.qk_cols) < (1L << 31),
+               "gemm: QKV fragment outputs must be under 2 GiB each");
   }
   CK_REQUIRE(d.rider.rows <= 0 || (conv && d.split > 1),
              "gemm: a rider GEMV goes with the split-K reduce of an implicit conv");

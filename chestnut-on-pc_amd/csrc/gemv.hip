@@ -322,6 +322,8 @@ void launch_frame_head(const QueueDims& q, const uint8_t* warped, const float* p
   c.Wo = (q.img_w - 1) / 2 + 1;
   const long per = (long)c.Ho * c.Wo * (Kp / 8);
   CK_REQUIRE(per < (1L << 30) && (long)q.img_h * q.img_w < (1L << 31), "frame_head: image too large");
+  // the patches leave through raw buffer stores addressed by 32-bit offsets
+  CK_REQUIRE(2L * 2 * c.Ho * c.Wo * Kp < (1L << 31), "frame_head: patch buffer must be under 2 GiB");
   c.blocks_per_image = (int)ceil_div(per, GEMV_THREADS);
   switch (ceil_div(K, GEMV_STEP_COLS)) {
     case 1: launch_head_nt<1>(pa, a, c, stream, slots, s); break;

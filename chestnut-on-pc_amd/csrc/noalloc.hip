@@ -75,6 +75,16 @@ extern "C" int ck_gemm_noalloc(const void* A, const void* B, float* C, const flo
                    std::to_string(plan.split) + "), above the " + std::to_string(ck::kScratchBytes) +
                    "-byte static scratch; use a smaller split_k or ck_gemm with a workspace");
     if (need) {
+      // the cached address is the current device's copy of the array; the
+      // kernels run on the stream's device, so the two must be the same GPU
+      if (stream) {
+        hipDevice_t sdev = -1;
+        int cur = -1;
+        CK_HIP(hipStreamGetDevice(static_cast<hipStream_t>(stream), &sdev));
+        CK_HIP(hipGetDevice(&cur));
+        CK_REQUIRE(sdev == cur, "ck_gemm_noalloc: the stream belongs to device " + std::to_string(sdev) +
+                                    ", not the current device " + std::to_string(cur));
+      }
       d.ws = ck::scratch_on_current_device();
       d.ws_floats = ck::kScratchBytes / sizeof(float);
     }

@@ -180,6 +180,8 @@ void launch_im2col_u8(const uint8_t* img, int batch, int C, int H, int W, half_t
   const int Ho = (H - 1) / 2 + 1, Wo = (W - 1) / 2 + 1;
   const long per = (long)Ho * Wo * (Kp / 8);
   CK_REQUIRE(per < (1L << 31) && (long)H * W < (1L << 31), "im2col_u8: image too large");
+  // the patches leave through raw buffer stores addressed by 32-bit offsets
+  CK_REQUIRE(2L * batch * Ho * Wo * Kp < (1L << 31), "im2col_u8: patch buffer must be under 2 GiB");
   CK_LAUNCH(im2col_u8_kernel, dim3(ceil_div(per, 256), batch), dim3(256), 0, s, img, C, H, W, patches, Kp,
                      Ho, Wo);
   CK_LAUNCHED("im2col_u8");

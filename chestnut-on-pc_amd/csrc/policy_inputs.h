@@ -108,6 +108,9 @@ inline PolicyArgs make_policy_args(const QueueDims& q, const uint8_t* warped, co
   const long frame_bytes = 6L * q.img_h * q.img_w;
   CK_REQUIRE(frame_bytes % 16 == 0, "policy_inputs: frame size must be a multiple of 16 bytes");
   CK_REQUIRE(q.img_slots == q.fs + 1, "policy_inputs: two sampled frames expected (fs*(2-1)+1 slots)");
+  // the image copies leave through raw buffer stores addressed by 32-bit offsets
+  CK_REQUIRE(4L * frame_bytes < (1L << 31) && 2L * q.img_slots * frame_bytes < (1L << 31),
+             "policy_inputs: image buffers must be under 2 GiB");
   PolicyArgs a;
   a.warped = warped; a.packed = packed; a.counter = counter;
   a.img_ring = img_ring; a.feat_ring = feat_ring; a.desire_ring = desire_ring;

@@ -85,3 +85,39 @@ def test_noalloc_gemm_rejects_workspace_above_scratch(gpu):
         _lib.call('ck_gemm_noalloc', _p(A), _p(B), _p(C), None, M, N, K, K, K, N, 0, 1, 8, _stream(torch))
     # nothing ran: C still zero
     assert not C.any().item()
+
+
+def test_noalloc_gemm_under_graph_capture(gpu):
+    """ck_gemm_noalloc captured into a graph (torch.cuda.graph, the current
+    stream being the capture stream) and replayed three times: every replay
+    is bit-identical to the eager call, with an eager call on another shape
+    between the replays overwriting the shared scratch, so a replay reads
+    only what it wrote itself."""
+    torch = gpu
+    rng = np.random.default_rng(5)
+    M, N, K = 1024, 1024, 6144
+    A = torch.from_numpy((rng.standard_normal((M, K)) / np.sqrt(K)).astype(np.float16)).cuda()
+    B = torch.from_numpy((rng.standard_normal((K, N)) / 2).astype(np.float16)).cuda()
+    C_eager = torch.full((M, N), float('nan'), dtype=torch.float32, device='cuda')
+    print('[noalloc] graph: eager call (looks up the scratch address)', flush=True)
+    _lib.call('ck_gemm_noalloc', _p(A), _p(B), _p(C_eager), None, M, N, K, K, N, N, 1, 0, 0, _stream(torch))
+    torch.cuda.synchronize()
+    A2 = torch.from_numpy((rng.standard_normal((256, 1024)) / 32).astype(np.float16)).cuda()
+    B2 = torch.from_numpy((rng.standard_normal((384, 1024)) / 2).astype(np.float16)).cuda()
+    C2 = torch.empty(256, 384, dtype=torch.float32, device='cuda')
+    C = torch.full((M, N), float('nan'), dtype=torch.float32, device='cuda')
+    g = torch.cuda.CUDAGraph()
+    print('[noalloc] graph: capture', flush=True)
+    with torch.cuda.graph(g):
+        _lib.call('ck_gemm_noalloc', _p(A), _p(B), _p(C), None, M, N, K, K, N, N, 1, 0, 0, _stream(torch))
+    torch.cuda.synchronize()
+    ref = C_eager.cpu().numpy()
+    for r in range(3):
+        C.fill_(float('nan'))
+        _lib.call('ck_gemm_noalloc', _p(A2), _p(B2), _p(C2), None, 256, 384, 1024, 1024, 1024, 384, 0, 0, 2,
+                  _stream(torch))
+        torch.cuda.synchronize()
+        print(f'[noalloc] graph: replay {r}', flush=True)
+        g.replay()
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(C.cpu().numpy(), ref)
