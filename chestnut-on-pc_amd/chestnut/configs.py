@@ -1,6 +1,6 @@
 """BASELINE configs 1-3 as stand-alone workloads for timing and rocprofv3.
 
-    python -m chestnut.configs --config 1|2|3 [--reps N] [--warmup-ms MS] [--out PATH]
+    python -m chestnut.configs --config 1|2|3|chain [--reps N] [--warmup-ms MS] [--out PATH]
 
 Each run first copies 256 MiB device to device (the calibration dispatch the
 FETCH_SIZE / WRITE_SIZE summaries scale by), runs the config's kernels
@@ -19,6 +19,11 @@ counter passes.
   3  one pre-LN block of the 1B model (d 2048, 16 x 128 heads, T 512, MLP
      8192), x ~ N(0, 1): the plan entries blkL.ln1 .. blk(L+1).ln1 of a
      4-block engine, each block with its own 100 MB of weights
+  chain  the cost of a dependent launch (ck_time_launch_chain): chains of
+     1000 launches of a near-empty kernel on 1, 256 and 1024 workgroups,
+     plain and as one graph; and frame-sized graphs (38 launches, the 39M
+     frame's dispatch count) replayed 200 times, whose per-launch cost less
+     the long chain's is the fixed cost of one graph launch
 """
 import argparse
 import json
@@ -151,9 +156,32 @@ def config3(torch, reps, warmup_ms=0):
         eng.close()
 
 
+def launch_chain(torch, reps=0, warmup_ms=0):
+    import ctypes
+    from ._lib import call
+    stream = None   # the call runs on a stream of its own
+
+    def us(n, wgs, mode, r):
+        v = ctypes.c_float()
+        call('ck_time_launch_chain', n, wgs, mode, r, ctypes.byref(v), stream)
+        return round(v.value, 3)
+    n = 1000
+    res = {'config': 'chain', 'workload': 'dependent launches of a near-empty kernel', 'n_launches': n,
+           'chain_us_per_launch': {}}
+    for wgs in (1, 256, 1024):
+        res['chain_us_per_launch'][str(wgs)] = {'plain': us(n, wgs, 0, 3), 'graph': us(n, wgs, 1, 3)}
+    f = 38
+    g_frame = us(f, 256, 1, 200)
+    g_long = res['chain_us_per_launch']['256']['graph']
+    res['frame_graph'] = {'launches_per_graph': f, 'replays': 200, 'graph_us_per_launch': g_frame,
+                          'plain_us_per_launch': us(f, 256, 0, 200),
+                          'fixed_us_per_graph_launch': round((g_frame - g_long) * f, 2)}
+    return res
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(prog='python -m chestnut.configs')
-    ap.add_argument('--config', type=int, required=True, choices=(1, 2, 3))
+    ap.add_argument('--config', required=True, choices=('1', '2', '3', 'chain'))
     ap.add_argument('--reps', type=int, default=0, help='timed launches (default: 120 / 200 / 10)')
     ap.add_argument('--warmup-ms', type=float, default=300.0,
                     help='untimed repetitions for about this much GPU time before the timed ones')
@@ -164,8 +192,12 @@ def main(argv=None):
         raise SystemExit('chestnut.configs needs a GPU')
     calibration_copy(torch)
     t0 = time.perf_counter()
-    reps = a.reps or {1: 120, 2: 200, 3: 10}[a.config]
-    res = {1: config1, 2: config2, 3: config3}[a.config](torch, reps, a.warmup_ms)
+    if a.config == 'chain':
+        res = launch_chain(torch)
+    else:
+        cfg = int(a.config)
+        reps = a.reps or {1: 120, 2: 200, 3: 10}[cfg]
+        res = {1: config1, 2: config2, 3: config3}[cfg](torch, reps, a.warmup_ms)
     res['warmup_ms'] = a.warmup_ms
     res['copy_bytes'] = COPY_BYTES
     res['wall_s'] = round(time.perf_counter() - t0, 3)

@@ -238,6 +238,13 @@ int ck_kernel_times(ck_engine* e, float* ms, int n) {
   CK_API_END
 }
 
+int ck_time_launch_chain(int n_launches, int workgroups, int mode, int reps, float* us_per_launch, void* stream) {
+  CK_API_BEGIN
+  CK_REQUIRE(us_per_launch, "null argument");
+  *us_per_launch = time_launch_chain(n_launches, workgroups, mode, reps, as_stream(stream));
+  CK_API_END
+}
+
 int ck_state_hashes(ck_engine* e, uint64_t* out, int n) {
   CK_API_BEGIN
   CK_REQUIRE(e && out, "null argument");

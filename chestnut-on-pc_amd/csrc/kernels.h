@@ -184,6 +184,12 @@ void launch_frame_head(const QueueDims& q, const uint8_t* warped, const float* p
 void launch_im2col_f16(const half_t* act, int batch, int C, int H, int W, half_t* patches, int Kp, hipStream_t s);
 void launch_tokens(const half_t* stem_out, int n_spatial, int C5, half_t* F, hipStream_t s);
 
+// ---- dependent-launch cost (chain.hip) ---------------------------------------
+// us per launch of `reps` repetitions of a chain of n dependent launches of a
+// near-empty kernel on `workgroups` workgroups: mode 0 plain launches, mode 1
+// the chain captured once as a graph and replayed.  Synchronises s.
+float time_launch_chain(int n, int workgroups, int mode, int reps, hipStream_t s);
+
 // ---- content hash of device tensors (hash.hip) --------------------------------
 constexpr int HASH_SPAN_BYTES = 64 << 10;
 struct HashSpan {

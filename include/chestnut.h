@@ -161,6 +161,18 @@ int ck_state_info(ck_engine* e, int i, char* name, size_t name_len, size_t* nbyt
  * (run_pinned2.py:1519-1542) and research/xcheck.py's per-argument hashes
  * (research/xcheck.py:65-124). */
 int ck_state_hashes(ck_engine* e, uint64_t* out, int n);
+
+/* The cost of a dependent launch: `reps` repetitions of a chain of n_launches
+ * launches of a near-empty kernel over `workgroups` workgroups, each ordered
+ * after the previous one on `stream`; mode 0 = plain launches, 1 = the chain
+ * captured once as a graph and replayed (one graph launch per repetition).
+ * *us_per_launch = elapsed time / (n_launches * reps), HIP events on stream
+ * (a null stream: a stream the call creates and destroys, since the null
+ * stream cannot be captured).
+ * Replaces: the reference's launch-cost measurements of its frame plan,
+ * ~0.5 ms per frame outside a CUDA graph, ~1.6 us per launch inside
+ * (README.md:20-26, 73; NOTES.md:48-50). */
+int ck_time_launch_chain(int n_launches, int workgroups, int mode, int reps, float* us_per_launch, void* stream);
 int ck_read_tensor(ck_engine* e, const char* name, void* host, size_t nbytes);
 int ck_write_tensor(ck_engine* e, const char* name, const void* host, size_t nbytes);
 
