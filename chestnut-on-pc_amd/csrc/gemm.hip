@@ -659,9 +659,12 @@ __global__ __launch_bounds__(64 * NWG * KG) void gemm_dma_kernel(const GemmParam
   // The B (weight) stream of the tiles with 128 or more rows -- the 1B model's
   // block GEMMs, 8-34 MB of weights each -- is loaded non-temporal: -1.3% of
   // the 1B frame.  Smaller tiles serve GEMMs whose few MB of weights the other
-  // workgroups reuse from the caches (the 39M model: +2.4% with it), and the
-  // [K][N] path keeps the default policy.
-  constexpr int BPOL = (BM >= 128 && !BT) ? 2 : 0;
+  // workgroups reuse from the caches (the 39M model: +2.4% with it).  The
+  // [K][N] B of config 1 streams non-temporal too: 32.1 -> 31.4 us.  (What
+  // still separates that kernel from the [N][K] one is texture-data time --
+  // TD busy 12.3 M against 8.8 M cycles for the same L2 requests -- not LDS
+  // bank conflicts, of which it has fewer.)
+  constexpr int BPOL = BM >= 128 ? 2 : 0;
   __shared__ __attribute__((aligned(1024))) half_t lds[S * STAGE];
   constexpr int WM = BM / (NWG / 2), WN = BN / 2;
   constexpr int FM = WM / 32, FN = WN / 32;
