@@ -382,7 +382,8 @@ def main():
     ap.add_argument('--dump-plan', default=None, help='write the frame plan (name, kernel, flops, bytes) as JSON')
     ap.add_argument('--pmc-run', default=None, metavar='FAMILY',
                     help='counter run: one frame, a 256 MiB device copy, then the first plan entry of each '
-                         'comma-separated FAMILY alone --pmc-reps times; writes --pmc-out and exits')
+                         'comma-separated FAMILY (or the entry of that exact name, e.g. blk1.ln1) alone '
+                         '--pmc-reps times; writes --pmc-out and exits')
     ap.add_argument('--pmc-reps', type=int, default=10)
     ap.add_argument('--pmc-out', default='gpurun_out/pmc_run.json')
     a = ap.parse_args()
@@ -423,7 +424,9 @@ def main():
         torch.cuda.synchronize()
         entries = []
         for fam in a.pmc_run.split(','):
-            idx = next(i for i, e in enumerate(plan) if family(e['name']) == fam)
+            idx = next((i for i, e in enumerate(plan) if e['name'] == fam), None)
+            if idx is None:
+                idx = next(i for i, e in enumerate(plan) if family(e['name']) == fam)
             for _ in range(a.pmc_reps):
                 eng.run_range(idx, idx + 1)
             eng.synchronize()
