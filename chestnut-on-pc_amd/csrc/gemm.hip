@@ -23,6 +23,8 @@
 // MFMA 32x32x16 operand layout (lane l of 64): A row l%32, k = 8*(l/32)..+7;
 // B column l%32, same k; D element e of lane l is row 8*(e/4) + 4*(l/32) +
 // e%4, column l%32.  The layout is checked by the MFMA KAT (wmma.hip).
+#include <type_traits>
+
 #include "common.h"
 #include "gemv_block.h"
 #include "kernels.h"
@@ -927,6 +929,229 @@ __global__ __launch_bounds__(64 * NWG * KG) void gemm_dma_kernel(const GemmParam
       }
 }
 
+// [K][N] B through registers (tile 2: 128x64, two K-groups of 4 waves, a
+// 6-stage ring, 3 stages per group).  A streams into LDS by LDS-DMA as in
+// gemm_dma_kernel.  B does not: each thread of a group loads a 2 (k) x 8 (n)
+// block of the step's 64 x 64 B tile with two 16-byte non-temporal loads
+// (8 consecutive threads cover one 128-byte k-row), issued three K-steps
+// ahead into registers; one step ahead of its use it interleaves the two rows
+// into 8 dwords (column n: B[k][n], B[k+1][n]) and writes them into the B
+// stage in an [N][K] layout, so the MFMA B fragments are plain 16-byte LDS
+// reads.  Its rows are XOR-swizzled by chunk ^ (((n >> 1) ^ (n >> 4)) & 7)
+// rather than the NT kernel's (n >> 1) & 7, and the upper half-wave writes
+// its columns in the order j ^ 1: both the fragment reads (16 consecutive
+// rows per pass) and the dword writes (64 lanes = 8 n-octets x 8 k-pairs)
+// then touch every bank at most once (a CPU replay checks both).  The transposing LDS reads of the
+// direct [K][N] path spend texture-data cycles (TD busy twice that of the
+// [N][K] kernel for the same L2 requests); this path does not.
+// Per group step t (group step u = global step 2u + group):
+//   top:   wait for A(t) and B(t+1) (everything issued before step t-1), barrier
+//   then:  B(t+1) registers -> its LDS stage (read at step t-2, retired by
+//          the barrier of step t-1); load B(t+3); A(t+2) spread over the
+//          k-slices of step t; the MFMAs of step t.
+// The buffers rotate with period 3, so the loop body is instantiated per
+// buffer phase (static register indices), and the group's step count is a
+// multiple of 3 (checked on the host).  The loop is branch-free -- every
+// step issues its B loads and A refill, the ones past the last step with the
+// step index clamped, into stages no later step reads -- so the compiler's
+// own wait counts for the register loads are exact (a branch in the loop
+// makes it fall back to draining every load).
+template <int I, class T>
+__device__ __forceinline__ T& pick3(T& a, T& b, T& c) {
+  if constexpr (I == 0) return a;
+  else if constexpr (I == 1) return b;
+  else return c;
+}
+
+__global__ __launch_bounds__(512) void gemm_kn_rb_kernel(const GemmParams p) {
+  constexpr int BM = 128, BN = 64, S = 6, KG = 2, NWG = 4;
+  constexpr int STAGE_A = BM * BK, STAGE_B = BN * BK, STAGE = STAGE_A + STAGE_B;   // halves
+  constexpr int WM = BM / 2, WN = BN / 2, FM = WM / 32, FN = WN / 32;
+  constexpr int NIA = BM / (8 * NWG);   // A LDS-DMA instructions per wave per step
+  constexpr int NBL = 2;                // B register loads per lane per step
+  constexpr int KS = BK / 16;
+  __shared__ __attribute__((aligned(1024))) half_t lds[S * STAGE];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int grp = wave / NWG, w4 = wave % NWG;
+  const int wm = w4 >> 1, wn = w4 & 1;
+  const int total = p.Mt * p.Nt * p.split * p.batch;
+  int L = blockIdx.x;
+  if ((total & 7) == 0) L = (L & 7) * (total >> 3) + (L >> 3);
+  const int mt = L % p.Mt; L /= p.Mt;
+  const int nt = L % p.Nt; L /= p.Nt;
+  const int sp = L % p.split;
+  const int bz = L / p.split;
+  const int m0 = mt * BM, n0 = nt * BN;
+  const int kbeg = sp * p.kps;
+  const int nkg = p.kps / (BK * KG);
+
+  const half_t* asrc[NIA];
+#pragma unroll
+  for (int i = 0; i < NIA; ++i) {
+    const int r = (w4 * NIA + i) * 8 + (lane >> 3);
+    const int q = (lane & 7) ^ ((r >> 1) & 7);
+    asrc[i] = p.A + bz * p.sA + (long)min(m0 + r, p.M - 1) * p.lda + kbeg + q * 8;
+  }
+  const half_t* const bnone[1] = {nullptr};
+  // B: group thread tg -> k-pair kp (rows 2kp, 2kp+1 of the step), n-octet no
+  const int tg = w4 * 64 + lane, kp = tg >> 3, no = tg & 7;
+  const half_t* const bsr = p.B + bz * p.sB + (long)(kbeg + 2 * kp) * p.ldb + n0 + 8 * no;
+  // write j of the lane: column 8no + (j ^ x), x = upper half-wave; its LDS
+  // offset (halves, in a stage's B part) and the byte selector that takes the
+  // column's half of each row word (v_perm_b32: low halves 0x05040100, high 0x07060302)
+  const int x = lane >> 5;
+  int bw[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int n = 8 * no + (j ^ x);
+    bw[j] = n * BK + ((((2 * kp) >> 3) ^ (((n >> 1) ^ (n >> 4)) & 7)) << 3) + ((2 * kp) & 7);
+  }
+  const unsigned bsel[2] = {x ? 0x07060302u : 0x05040100u, x ? 0x05040100u : 0x07060302u};
+  float16_t acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = float16_t{};
+  // accumulators hold D^T (operands swapped): lane's 4 consecutive e = 4 columns of one row
+  constexpr int NBC = 16;
+  float bcol[FN][NBC];
+  {
+    const float* bias = (p.split == 1 && p.bias) ? p.bias + bz * p.sBias : nullptr;
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int e = 0; e < NBC; ++e) {
+        const int n = n0 + wn * WN + j * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+        bcol[j][e] = (bias && n < p.N) ? bias[n] : 0.f;
+      }
+  }
+  auto stage_of = [&](int u) { return lds + ((KG * u + grp) % S) * STAGE; };
+  auto b_load = [&](u32x4_t (&r)[NBL], int u) {
+    const half_t* src = bsr + (long)(KG * u + grp) * BK * p.ldb;
+    r[0] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(src));
+    r[1] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(src + p.ldb));
+  };
+  auto b_store = [&](const u32x4_t (&r)[NBL], int u) {
+    half_t* st = stage_of(u) + STAGE_A;
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      *reinterpret_cast<unsigned*>(st + bw[j]) = __builtin_amdgcn_perm(r[1][j >> 1], r[0][j >> 1], bsel[j & 1]);
+  };
+  u32x4_t rb0[NBL], rb1[NBL], rb2[NBL];
+  // prologue (nkg >= 3): B(0), B(1), A(0), B(2), A(1); then everything has landed and B(0) goes to LDS
+  b_load(rb0, 0);
+  b_load(rb1, 1);
+  dma_issue<NIA, 0, STAGE_A>(asrc, bnone, stage_of(0), w4, grp * BK, 0);
+  b_load(rb2, 2);
+  dma_issue<NIA, 0, STAGE_A>(asrc, bnone, stage_of(1), w4, (KG + grp) * BK, 0);
+  wait_vm_lgkm0<0>();
+  b_store(rb0, 0);
+
+  int aoff[FM], boff[FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i) aoff[i] = (wm * WM + i * 32 + (lane & 31)) * BK;
+  int bsw[FN];   // the B rows' swizzle, ((n >> 1) ^ (n >> 4)) & 7
+#pragma unroll
+  for (int j = 0; j < FN; ++j) {
+    const int n = wn * WN + j * 32 + (lane & 31);
+    boff[j] = n * BK;
+    bsw[j] = ((n >> 1) ^ (n >> 4)) & 7;
+  }
+  const int rsw = (lane >> 1) & 7;
+
+  // one group step; PH = t % 3: B(t+1) is in buffer (PH+1)%3, B(t+3) loads into PH
+  auto step = [&](auto ph, int t) {
+    constexpr int PH = decltype(ph)::value;
+    auto& rs = pick3<(PH + 1) % 3>(rb0, rb1, rb2);
+    auto& rl = pick3<PH>(rb0, rb1, rb2);
+    // everything but the previous step's NIA + NBL loads has landed: A(t), B(t+1)
+    wait_vm_lgkm0<NIA + NBL>();
+    lds_barrier();
+    b_store(rs, t + 1);                 // past the last step: a stage no later step reads
+    b_load(rl, min(t + 3, nkg - 1));
+    half_t* const rst = stage_of(t + 2);
+    const int rko = (KG * min(t + 2, nkg - 1) + grp) * BK;
+    const half_t* sa = stage_of(t);
+    const half_t* sb = sa + STAGE_A;
+    half8_t af[KS][FM], bf[KS][FN];
+    auto read_slice = [&](int kk) {
+      const int c = kk * 2 + (lane >> 5);
+#pragma unroll
+      for (int i = 0; i < FM; ++i) af[kk][i] = *reinterpret_cast<const half8_t*>(sa + aoff[i] + ((c ^ rsw) << 3));
+#pragma unroll
+      for (int j = 0; j < FN; ++j) bf[kk][j] = *reinterpret_cast<const half8_t*>(sb + boff[j] + ((c ^ bsw[j]) << 3));
+    };
+    read_slice(0);
+    read_slice(1);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int kk = 0; kk < KS; ++kk) {
+      dma_issue_range<NIA, 0, STAGE_A>(asrc, bnone, rst, w4, rko, 0, kk * NIA / KS, (kk + 1) * NIA / KS);
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(bf[kk][j], af[kk][i], acc[i][j], 0, 0, 0);
+      if (kk + 2 < KS) read_slice(kk + 2);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  for (int t = 0; t < nkg; t += 3) {
+    step(std::integral_constant<int, 0>{}, t);
+    step(std::integral_constant<int, 1>{}, t + 1);
+    step(std::integral_constant<int, 2>{}, t + 2);
+  }
+
+  // group 1 hands its partial tile to group 0 through LDS
+  {
+    float* red = reinterpret_cast<float*>(lds);
+    wait_vm_lgkm0<0>();
+    lds_barrier();
+    if (grp == 1) {
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) red[((w4 * FM * FN + i * FN + j) * 16 + e) * 64 + lane] = acc[i][j][e];
+    }
+    wait_vm_lgkm0<0>();
+    lds_barrier();
+    if (grp == 0) {
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) acc[i][j][e] += red[((w4 * FM * FN + i * FN + j) * 16 + e) * 64 + lane];
+    }
+    wait_vm_lgkm0<0>();
+    lds_barrier();
+    if (grp == 1) return;   // no barrier follows
+  }
+  if (p.vec) {
+    constexpr int REGION = WM * (WN + 8) * 4;
+    static_assert(NWG * REGION <= S * STAGE * 2, "LDS ring too small for the staged epilogue");
+    store_staged<WM, WN, FM, FN, EPI_F32, true, NBC>(p, acc, bcol, reinterpret_cast<char*>(lds) + w4 * REGION,
+                                                    m0 + wm * WM, n0 + wn * WN, sp, bz, lane);
+    return;
+  }
+  float* const out = p.split > 1 ? p.ws + ((long)sp * p.batch + bz) * (long)p.M * p.N
+                                 : static_cast<float*>(p.C) + bz * p.sC;
+  const long ld = p.split > 1 ? p.N : p.ldc;
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int m = m0 + wm * WM + i * 32 + (lane & 31);
+        const int n = n0 + wn * WN + j * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+        if (m < p.M && n < p.N) out[(long)m * ld + n] = acc[i][j][e] + bcol[j][e];
+      }
+}
+
 // B given as [K][N] (N contiguous, config 1's layout) is turned into the
 // [N][K] layout the LDS-DMA kernel streams: 64x64 tiles through LDS, 16-byte
 // global reads and writes.  The LDS pitch of 66 halves (33 words) keeps the
@@ -1001,6 +1226,7 @@ void launch_epi_cv(int tile, const GemmParams& p, hipStream_t s) {
 void launch_dma_bt(const GemmParams& p, int tile, bool kg2, hipStream_t s) {
   const int grid = p.Mt * p.Nt * p.split * p.batch;
   if (tile == 9) CK_LAUNCH((gemm_dma_kernel<256, 128, 3, 1, EPI_F32, 8, true>), dim3(grid), dim3(512), 0, s, p);
+  else if (tile == 2) CK_LAUNCH(gemm_kn_rb_kernel, dim3(grid), dim3(512), 0, s, p);
   else if (kg2) CK_LAUNCH((gemm_dma_kernel<128, 128, 4, 2, EPI_F32, 4, true>), dim3(grid), dim3(512), 0, s, p);
   else CK_LAUNCH((gemm_dma_kernel<128, 128, 5, 1, EPI_F32, 4, true>), dim3(grid), dim3(256), 0, s, p);
   CK_LAUNCHED("gemm_dma_bt");
@@ -1096,7 +1322,10 @@ void launch_reduce(const GemmParams& p, hipStream_t s, const GemvRider* rider = 
 // it lies and read transposed (no transpose pass, no workspace for it).
 // (A and B are required to be 16-byte aligned for every launch.)
 bool bt_direct(const GemmDesc& d) {
-  if (!d.b_kn || d.N % 128 != 0) return false;
+  if (!d.b_kn) return false;
+  if (d.tile == 2)   // B through registers: whole 3-step phases of two K-groups
+    return d.N % 64 == 0 && (d.K / d.split) % (6 * BK) == 0;
+  if (d.N % 128 != 0) return false;
   if (d.tile == 1) return (d.K / d.split) % (2 * BK) == 0;
   return d.tile == 9;   // 256x128, 8 waves in one K-group
 }
@@ -1111,6 +1340,20 @@ int tile_bn(int tile) { return tile == 9 ? 128 : (tile_base(tile) == 1 || tile_b
 size_t gemm_plan(GemmDesc& d) {
   CK_REQUIRE(d.M > 0 && d.N > 0 && d.K > 0 && d.batch > 0, "gemm: empty problem");
   CK_REQUIRE(d.K % BK == 0, "gemm: K must be a multiple of 64 (pad K)");
+  if (d.tile == 0 && d.b_kn && d.split == 0 && d.N % 64 == 0) {
+    // A [K][N] B with enough 128x64 tiles to fill the GPU at a split whose K
+    // per split makes whole 3-step phases of the register-staged kernel:
+    // that kernel (config 1: 30.0-31.3 us at split 2, against 31.2-32.6 us
+    // for the 128x128 transposing-read tile at split 4).
+    const long t2 = (long)ceil_div(d.M, 128) * (d.N / 64) * d.batch;
+    int s2 = 0;
+    for (int c = 1; c <= 8; ++c)
+      if (t2 * c <= 256 && d.K % (c * 6 * BK) == 0) s2 = c;
+    if (t2 >= 64 && s2 > 0) {
+      d.tile = 2;
+      d.split = s2;
+    }
+  }
   if (d.tile == 0) {
     // 128-wide tiles unless a dimension is small; 64x64 when 128-wide tiles
     // leave most of the 256 CUs without a tile.

@@ -78,3 +78,46 @@ def test_transposed_reads_use_each_bank_at_most_twice():
                     for bank in ((o * 2 // 4) % 64, (o * 2 // 4 + 1) % 64):   # 8 bytes = 2 banks
                         hits[bank] = hits.get(bank, 0) + 1
                 assert max(hits.values()) <= 2 and len(hits) == 64
+
+
+def test_register_staged_b_layout_and_banks():
+    """gemm_kn_rb_kernel: group thread tg (lane l of wave w, tg = 64w + l) holds
+    rows 2kp, 2kp+1 (kp = tg >> 3) of columns 8no .. 8no+7 (no = tg & 7) of
+    the step's 64 x 64 [K][N] B tile; its write j puts column n = 8no + (j ^ x)
+    (x = l >> 5) as the dword (B[k][n], B[k+1][n]), k = 2kp, at halves offset
+    n*64 + ((k>>3) ^ f(n))*8 + (k&7), f(n) = ((n>>1) ^ (n>>4)) & 7.  The 256
+    threads x 8 writes must fill every half of the stage once, as the [N][K]
+    layout the 16-byte fragment reads address (row n, physical chunk =
+    chunk ^ f(n)); every write instruction's 64 lanes must hit 64 distinct
+    banks, and every fragment read's 16-lane pass (rows base + l%32, chunk
+    2kk + l/32) 64 distinct banks."""
+    f = lambda n: ((n >> 1) ^ (n >> 4)) & 7                     # noqa: E731
+    bank = lambda h: (h * 2 // 4) % 64                           # noqa: E731
+    rng = np.random.default_rng(3)
+    B = rng.integers(0, 1 << 30, (64, 64))
+    lds = np.full(64 * 64, -1, np.int64)
+    for w in range(4):
+        for j in range(8):
+            banks = set()
+            for lane in range(64):
+                tg = 64 * w + lane
+                kp, no, x = tg >> 3, tg & 7, lane >> 5
+                n, k = 8 * no + (j ^ x), 2 * kp
+                off = n * 64 + (((k >> 3) ^ f(n)) << 3) + (k & 7)
+                assert lds[off] == -1 and lds[off + 1] == -1
+                lds[off], lds[off + 1] = B[k, n], B[k + 1, n]
+                banks.add(bank(off))
+            assert len(banks) == 64
+    assert (lds >= 0).all()
+    for n in range(64):
+        for k in range(64):
+            assert lds[n * 64 + (((k >> 3) ^ f(n)) << 3) + (k & 7)] == B[k, n]
+    for base in (0, 32):
+        for kk in range(4):
+            for p in range(4):
+                banks = []
+                for lane in range(16 * p, 16 * p + 16):
+                    n, c = base + (lane & 31), 2 * kk + (lane >> 5)
+                    o = n * 64 + ((c ^ f(n)) << 3)
+                    banks += [(bank(o) + d) % 64 for d in range(4)]
+                assert sorted(banks) == list(range(64))

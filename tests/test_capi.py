@@ -86,11 +86,18 @@ def test_kernel_entry_validation_rejects_before_launch():
 
 def test_gemm_planner_host_logic():
     t, s, nb = ctypes.c_int(0), ctypes.c_int(0), ctypes.c_size_t()
-    # config 1: 1024 x 1024 output, K = 6144 -> 64 tiles of 128x128, split to fill 256 CUs
+    # config 1: 1024 x 1024 output, K = 6144, [K][N] B -> 128 tiles of 128x64 (B through
+    # registers), split 2 to fill 256 CUs; workspace: the 2 partial planes, no transposed B
     _lib.call('ck_gemm_workspace', 1024, 1024, 6144, 1, ctypes.byref(t), ctypes.byref(s), ctypes.byref(nb))
-    # workspace: the 4 split-K partial planes only (tile 1 reads the [K][N] B
-    # transposed out of LDS, no transposed copy)
+    assert t.value == 2 and s.value == 2 and nb.value == 2 * 1024 * 1024 * 4
+    # the same with B as [N][K]: 64 tiles of 128x128, split 4
+    t, s = ctypes.c_int(0), ctypes.c_int(0)
+    _lib.call('ck_gemm_workspace', 1024, 1024, 6144, 0, ctypes.byref(t), ctypes.byref(s), ctypes.byref(nb))
     assert t.value == 1 and s.value == 4 and nb.value == 4 * 1024 * 1024 * 4
+    # tile 1 reads the [K][N] B transposed out of LDS: the partial planes only
+    t, s = ctypes.c_int(1), ctypes.c_int(4)
+    _lib.call('ck_gemm_workspace', 1024, 1024, 6144, 1, ctypes.byref(t), ctypes.byref(s), ctypes.byref(nb))
+    assert nb.value == 4 * 1024 * 1024 * 4
     # one K-group (tile 5) transposes B into the workspace tail first
     t, s = ctypes.c_int(5), ctypes.c_int(4)
     _lib.call('ck_gemm_workspace', 1024, 1024, 6144, 1, ctypes.byref(t), ctypes.byref(s), ctypes.byref(nb))

@@ -168,18 +168,25 @@ def test_gemm_config1_full_size(gpu):
     # same problem with B stored [N][K]
     Ct = host(K.gemm(Ad, dev(gpu, np.ascontiguousarray(B.T)), b_kn=False))
     _gemm_check(Ct, A, B)
+    # the 128x64 tile at split 2, B loaded through registers (deterministic too)
+    C2 = host(K.gemm(Ad, Bd, b_kn=True, tile=2, split_k=2))
+    _gemm_check(C2, A, B)
+    np.testing.assert_array_equal(host(K.gemm(Ad, Bd, b_kn=True, tile=2, split_k=2)), C2)
 
 
-@pytest.mark.parametrize('tile', [0, 1, 4, 5, 9, 11, 13])
+@pytest.mark.parametrize('tile', [0, 1, 2, 4, 5, 9, 11, 13])
 @pytest.mark.parametrize('M,N,Kd,split', [(100, 200, 320, 1), (300, 136, 1024, 2), (100, 256, 384, 1),
-                                          (300, 384, 1024, 4), (64, 128, 256, 2)])
+                                          (300, 384, 1024, 4), (64, 128, 256, 2), (300, 192, 768, 1),
+                                          (64, 128, 1536, 2)])
 def test_gemm_kn_paths(gpu, tile, M, N, Kd, split):
     """[K][N] B: with N a multiple of 128 the two-K-group 128x128 LDS-DMA
     tile (1, and 0 when it picks it) and the 8-wave 256x128 tile (9) stream
-    it into LDS as it is and read their MFMA fragments transposed; otherwise
-    the LDS-DMA tiles (4, 5, 9, ...) transpose it into the workspace first,
-    and the register-staged tiles (11, 13) transpose it in registers; ragged
-    M and N."""
+    it into LDS as it is and read their MFMA fragments transposed; the
+    128x64 tile (2) with N a multiple of 64 and K per split a multiple of 384
+    loads it through registers and writes it to LDS in the [N][K] layout;
+    otherwise the LDS-DMA tiles (2, 4, 5, 9, ...) transpose it into the
+    workspace first, and the register-staged tiles (11, 13) transpose it in
+    registers; ragged M and N."""
     from chestnut import kernels as K
     rng = np.random.default_rng(M + N + tile)
     A = rng.standard_normal((M, Kd)).astype(np.float16)

@@ -54,8 +54,8 @@ def _case(torch, M, N, K, b_kn, tile, split, seed, with_bias):
 
 def test_noalloc_gemm_two_calls_match_ck_gemm(gpu):
     torch = gpu
-    # 1: BASELINE config 1 (1024 x 6144 x 1024, [K][N] B): tile 1, split 4,
-    #    16 MiB of partials in the scratch
+    # 1: BASELINE config 1 (1024 x 6144 x 1024, [K][N] B): tile 2, split 2,
+    #    8 MiB of partials in the scratch
     print('[noalloc] call 1: 1024x1024x6144 b_kn', flush=True)
     A, B, _, got, ref, (t, s, nb) = _case(torch, 1024, 1024, 6144, 1, 0, 0, 1, False)
     assert s > 1 and nb > 0, 'the first case must use the scratch'
