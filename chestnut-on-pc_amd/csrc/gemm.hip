@@ -633,6 +633,68 @@ __device__ __forceinline__ void dma_issue_range(const half_t* const* asrc, const
 // 8 bytes per chunk, the fewest passes 512 bytes take.
 __device__ __forceinline__ int bt_swz(int row) { return ((row & 3) << 2) | ((row >> 3) & 1); }
 
+// The two K-groups' sum fused into the staged f32 epilogue (EPI_F32 and
+// EPI_PARTIALS on kernels with two K-groups of NWG waves): every wave stages
+// its group's sub-tile in a region of its own (group g, wave w: region
+// g * NWG + w), one barrier, then the two waves of sub-tile w write half of
+// its rows each, as 16-byte chunks of group 0 + group 1 (+ bias) -- the sum
+// the LDS hand-over forms (group 0's accumulators += group 1's) with one
+// barrier fewer, no 4-byte LDS traffic and the stores spread over both
+// groups.  Called by all 2 * NWG waves after their last ring read has
+// retired (barrier); base: the LDS ring.
+template <int WM, int WN, int FM, int FN, int EPI, bool SWP, int NWG>
+__device__ __forceinline__ void store_staged_kg2(const GemmParams& p, const float16_t (&acc)[FM][FN], char* base,
+                                                 int grp, int w4, int mw, int nw, int sp, int bz, int lane) {
+  static_assert(EPI == EPI_F32 || EPI == EPI_PARTIALS, "f32 outputs only");
+  constexpr int PF = WN + 8, REGION = WM * PF * 4, CPR = WN / 4;
+  float* st = reinterpret_cast<float*>(base + (grp * NWG + w4) * REGION);
+  if constexpr (SWP) {
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          float4_t v;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] = acc[i][j][4 * k + e];
+          *reinterpret_cast<float4_t*>(st + (i * 32 + (lane & 31)) * PF + j * 32 + 8 * k + 4 * (lane >> 5)) = v;
+        }
+  } else {
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int e = 0; e < 16; ++e)
+          st[(i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3)) * PF + j * 32 + (lane & 31)] = acc[i][j][e];
+  }
+  wait_vm_lgkm0<0>();
+  lds_barrier();
+  const float* s0 = reinterpret_cast<const float*>(base + w4 * REGION);
+  const float* s1 = reinterpret_cast<const float*>(base + (NWG + w4) * REGION);
+  const bool to_ws = p.split > 1 || EPI == EPI_PARTIALS;
+  float* dst = to_ws ? p.ws + ((long)sp * p.batch + bz) * (long)p.M * p.N : static_cast<float*>(p.C) + bz * p.sC;
+  const long ld = to_ws ? p.N : p.ldc;
+  const long plane = to_ws ? 4L * p.M * p.N : 4L * ((long)(p.M - 1) * p.ldc + p.N);
+  const bool sc1 = sc1_ok(plane);
+  const __amdgpu_buffer_rsrc_t rs = sc1_rsrc(dst, sc1 ? plane : 0);
+  const float* bias = (!to_ws && p.bias) ? p.bias + bz * p.sBias : nullptr;
+  constexpr int HR = WM / 2;   // rows per wave
+#pragma unroll 4
+  for (int q = lane; q < HR * CPR; q += 64) {
+    const int r = grp * HR + q / CPR, c = (q % CPR) * 4;
+    const int m = mw + r, n = nw + c;
+    if (m >= p.M || n >= p.N) continue;
+    float4_t v = *reinterpret_cast<const float4_t*>(s0 + r * PF + c) + *reinterpret_cast<const float4_t*>(s1 + r * PF + c);
+    if (bias)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] += bias[n + e];
+    if (sc1) store_sc1(rs, ((long)m * ld + n) * 4, v);
+    else __builtin_nontemporal_store(v, reinterpret_cast<float4_t*>(dst + (long)m * ld + n));
+  }
+}
+
 // KG K-groups of NWG waves each (64*NWG*KG threads): group g consumes
 // K-steps g, g+KG, g+2KG, ... through its own S/KG stages of the ring, so
 // KG=2 puts 8 waves on a CU for one output tile (twice the loads in flight)
@@ -859,6 +921,18 @@ __global__ __launch_bounds__(64 * NWG * KG) void gemm_dma_kernel(const GemmParam
     }
   }
 
+  // f32 outputs of two K-groups: the groups' sum inside the staged epilogue
+  constexpr bool KG2_STAGED =
+      KG == 2 && (EPI == EPI_F32 || EPI == EPI_PARTIALS) && 2 * NWG * WM * (WN + 8) * 4 <= S * STAGE * 2;
+  if constexpr (KG2_STAGED) {
+    if (p.vec) {
+      wait_vm_lgkm0<0>();   // every wave is past its last ring read
+      lds_barrier();
+      store_staged_kg2<WM, WN, FM, FN, EPI, SWP, NWG>(p, acc, reinterpret_cast<char*>(lds), grp, w4, m0 + wm * WM,
+                                                      n0 + wn * WN, sp, bz, lane);
+      return;
+    }
+  }
   if (KG > 1) {   // group 1 hands its partial tile to group 0 through LDS
     float* red = reinterpret_cast<float*>(lds);
     wait_vm_lgkm0<0>();
@@ -1026,18 +1100,20 @@ __global__ __launch_bounds__(512) void gemm_kn_rb_kernel(const GemmParams p) {
         bcol[j][e] = (bias && n < p.N) ? bias[n] : 0.f;
       }
   }
+  // stage of group step u: (KG u + grp) % S = 2 (u % 3) + grp
   auto stage_of = [&](int u) { return lds + ((KG * u + grp) % S) * STAGE; };
+  half_t* const gstage = lds + grp * STAGE;
   auto b_load = [&](u32x4_t (&r)[NBL], int u) {
     const half_t* src = bsr + (long)(KG * u + grp) * BK * p.ldb;
     r[0] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(src));
     r[1] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(src + p.ldb));
   };
-  auto b_store = [&](const u32x4_t (&r)[NBL], int u) {
-    half_t* st = stage_of(u) + STAGE_A;
+  auto b_store_at = [&](const u32x4_t (&r)[NBL], half_t* st) {
 #pragma unroll
     for (int j = 0; j < 8; ++j)
-      *reinterpret_cast<unsigned*>(st + bw[j]) = __builtin_amdgcn_perm(r[1][j >> 1], r[0][j >> 1], bsel[j & 1]);
+      *reinterpret_cast<unsigned*>(st + STAGE_A + bw[j]) = __builtin_amdgcn_perm(r[1][j >> 1], r[0][j >> 1], bsel[j & 1]);
   };
+  auto b_store = [&](const u32x4_t (&r)[NBL], int u) { b_store_at(r, stage_of(u)); };
   u32x4_t rb0[NBL], rb1[NBL], rb2[NBL];
   // prologue (nkg >= 3): B(0), B(1), A(0), B(2), A(1); then everything has landed and B(0) goes to LDS
   b_load(rb0, 0);
@@ -1060,19 +1136,25 @@ __global__ __launch_bounds__(512) void gemm_kn_rb_kernel(const GemmParams p) {
   }
   const int rsw = (lane >> 1) & 7;
 
-  // one group step; PH = t % 3: B(t+1) is in buffer (PH+1)%3, B(t+3) loads into PH
-  auto step = [&](auto ph, int t) {
+  // one group step; PH = t % 3: B(t+1) is in buffer (PH+1)%3, B(t+3) loads into PH.
+  // LAST: the final phase (steps nkg-3 .. nkg-1) loads nothing past the end:
+  // step nkg-3 refills A only, nkg-2 loads nothing, nkg-1 neither loads nor
+  // stores B, so nothing is in flight when the loop ends.
+  auto step = [&](auto ph, auto last, int t) {
     constexpr int PH = decltype(ph)::value;
+    constexpr bool LAST = decltype(last)::value;
     auto& rs = pick3<(PH + 1) % 3>(rb0, rb1, rb2);
     auto& rl = pick3<PH>(rb0, rb1, rb2);
-    // everything but the previous step's NIA + NBL loads has landed: A(t), B(t+1)
-    wait_vm_lgkm0<NIA + NBL>();
+    // everything but the previous step's loads has landed: A(t), B(t+1)
+    constexpr int PREV = !LAST || PH == 0 ? NIA + NBL : (PH == 1 ? NIA : 0);
+    wait_vm_lgkm0<PREV>();
     lds_barrier();
-    b_store(rs, t + 1);                 // past the last step: a stage no later step reads
-    b_load(rl, min(t + 3, nkg - 1));
-    half_t* const rst = stage_of(t + 2);
-    const int rko = (KG * min(t + 2, nkg - 1) + grp) * BK;
-    const half_t* sa = stage_of(t);
+    half_t* const st1 = gstage + 2 * ((PH + 1) % 3) * STAGE;   // stage of step t + 1
+    if constexpr (!LAST || PH < 2) b_store_at(rs, st1);
+    if constexpr (!LAST) b_load(rl, t + 3);
+    half_t* const rst = gstage + 2 * ((PH + 2) % 3) * STAGE;   // stage of step t + 2
+    const int rko = (KG * (t + 2) + grp) * BK;
+    const half_t* sa = gstage + 2 * PH * STAGE;
     const half_t* sb = sa + STAGE_A;
     half8_t af[KS][FM], bf[KS][FN];
     auto read_slice = [&](int kk) {
@@ -1087,7 +1169,8 @@ __global__ __launch_bounds__(512) void gemm_kn_rb_kernel(const GemmParams p) {
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int kk = 0; kk < KS; ++kk) {
-      dma_issue_range<NIA, 0, STAGE_A>(asrc, bnone, rst, w4, rko, 0, kk * NIA / KS, (kk + 1) * NIA / KS);
+      if constexpr (!LAST || PH == 0)
+        dma_issue_range<NIA, 0, STAGE_A>(asrc, bnone, rst, w4, rko, 0, kk * NIA / KS, (kk + 1) * NIA / KS);
 #pragma unroll
       for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -1097,12 +1180,28 @@ __global__ __launch_bounds__(512) void gemm_kn_rb_kernel(const GemmParams p) {
       __builtin_amdgcn_sched_barrier(0);
     }
   };
-  for (int t = 0; t < nkg; t += 3) {
-    step(std::integral_constant<int, 0>{}, t);
-    step(std::integral_constant<int, 1>{}, t + 1);
-    step(std::integral_constant<int, 2>{}, t + 2);
+  using P0 = std::integral_constant<int, 0>;
+  using P1 = std::integral_constant<int, 1>;
+  using P2 = std::integral_constant<int, 2>;
+  using Mid = std::false_type;
+  using Last = std::true_type;
+  for (int t = 0; t + 3 < nkg; t += 3) {
+    step(P0{}, Mid{}, t);
+    step(P1{}, Mid{}, t + 1);
+    step(P2{}, Mid{}, t + 2);
   }
+  step(P0{}, Last{}, nkg - 3);
+  step(P1{}, Last{}, nkg - 2);
+  step(P2{}, Last{}, nkg - 1);
 
+  if (p.vec) {   // the two groups' sum inside the staged epilogue
+    static_assert(2 * NWG * WM * (WN + 8) * 4 <= S * STAGE * 2, "LDS ring too small for the staged epilogue");
+    wait_vm_lgkm0<0>();
+    lds_barrier();
+    store_staged_kg2<WM, WN, FM, FN, EPI_F32, true, NWG>(p, acc, reinterpret_cast<char*>(lds), grp, w4, m0 + wm * WM,
+                                                         n0 + wn * WN, sp, bz, lane);
+    return;
+  }
   // group 1 hands its partial tile to group 0 through LDS
   {
     float* red = reinterpret_cast<float*>(lds);
@@ -1126,16 +1225,7 @@ __global__ __launch_bounds__(512) void gemm_kn_rb_kernel(const GemmParams p) {
 #pragma unroll
           for (int e = 0; e < 16; ++e) acc[i][j][e] += red[((w4 * FM * FN + i * FN + j) * 16 + e) * 64 + lane];
     }
-    wait_vm_lgkm0<0>();
-    lds_barrier();
-    if (grp == 1) return;   // no barrier follows
-  }
-  if (p.vec) {
-    constexpr int REGION = WM * (WN + 8) * 4;
-    static_assert(NWG * REGION <= S * STAGE * 2, "LDS ring too small for the staged epilogue");
-    store_staged<WM, WN, FM, FN, EPI_F32, true, NBC>(p, acc, bcol, reinterpret_cast<char*>(lds) + w4 * REGION,
-                                                    m0 + wm * WM, n0 + wn * WN, sp, bz, lane);
-    return;
+    if (grp == 1) return;
   }
   float* const out = p.split > 1 ? p.ws + ((long)sp * p.batch + bz) * (long)p.M * p.N
                                  : static_cast<float*>(p.C) + bz * p.sC;

@@ -174,6 +174,69 @@ def test_gemm_config1_full_size(gpu):
     np.testing.assert_array_equal(host(K.gemm(Ad, Bd, b_kn=True, tile=2, split_k=2)), C2)
 
 
+@pytest.mark.parametrize('b_kn,tile,M,N,Kd', [(True, 2, 1024, 1024, 6144), (False, 2, 1024, 1024, 6144),
+                                              (True, 2, 300, 192, 768), (True, 1, 300, 384, 1024),
+                                              (False, 1, 300, 520, 1024), (False, 4, 64, 128, 256),
+                                              (True, 5, 100, 200, 512)])
+@pytest.mark.parametrize('with_bias', [False, True])
+def test_gemm_split2_equals_sum_of_halves(gpu, b_kn, tile, M, N, Kd, with_bias):
+    """Split 2 with an f32 output is bit for bit (0 + p0) + p1 (+ bias), where
+    p0 and p1 are the split-1 products of the two K halves on the same tile:
+    the split-K reduce sums the partial planes in split order and adds the
+    bias last, on every one of ten launches."""
+    from chestnut import kernels as K
+    torch = gpu
+    print(f'[gemm] split-2 halves b_kn={b_kn} tile={tile} {M}x{N}x{Kd} bias={with_bias}', flush=True)
+    rng = np.random.default_rng(M + N + Kd + tile)
+    A = (rng.standard_normal((M, Kd)) / 16).astype(np.float16)
+    B = (rng.standard_normal((Kd, N) if b_kn else (N, Kd)) / 16).astype(np.float16)
+    b = rng.standard_normal(N).astype(np.float32) if with_bias else None
+    h = Kd // 2
+    Bh = (B[:h], B[h:]) if b_kn else (B[:, :h], B[:, h:])
+    p0 = host(K.gemm(dev(torch, A[:, :h]), dev(torch, Bh[0]), b_kn=b_kn, tile=tile, split_k=1))
+    p1 = host(K.gemm(dev(torch, A[:, h:]), dev(torch, Bh[1]), b_kn=b_kn, tile=tile, split_k=1))
+    want = (np.float32(0) + p0) + p1
+    if with_bias:
+        want = want + b
+    Ad, Bd, bd = dev(torch, A), dev(torch, B), (dev(torch, b) if with_bias else None)
+    C = torch.empty(M, N, device='cuda')
+    _, _, nb = K.gemm_workspace(M, N, Kd, b_kn, tile, 2)
+    ws = torch.empty(nb // 4, device='cuda')
+    for r in range(10):
+        # NaN in C and in the partial planes: a partial plane read before it
+        # was written would show up as NaN
+        C.fill_(float('nan'))
+        ws.fill_(float('nan'))
+        K.gemm(Ad, Bd, b_kn=b_kn, bias=bd, tile=tile, split_k=2, out=C, workspace=ws)
+        got = host(C)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), f'launch {r}'
+
+
+def test_gemm_split2_on_concurrent_streams(gpu):
+    """Split-K GEMMs in flight at once on two streams, each with its own
+    workspace: every result matches its single-stream value."""
+    from chestnut import kernels as K
+    torch = gpu
+    rng = np.random.default_rng(5)
+    M, N, Kd = 512, 512, 3072
+    As = [dev(torch, (rng.standard_normal((M, Kd)) / 16).astype(np.float16)) for _ in range(2)]
+    Bs = [dev(torch, (rng.standard_normal((Kd, N)) / 16).astype(np.float16)) for _ in range(2)]
+    want = [host(K.gemm(As[i], Bs[i], b_kn=True, tile=2, split_k=2)) for i in range(2)]
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    outs = [[torch.empty(M, N, device='cuda') for _ in range(8)] for _ in range(2)]
+    _, _, nb = K.gemm_workspace(M, N, Kd, True, 2, 2)
+    wss = [[torch.full((nb // 4,), float('nan'), device='cuda') for _ in range(8)] for _ in range(2)]
+    torch.cuda.synchronize()
+    for r in range(8):
+        for i in range(2):
+            with torch.cuda.stream(streams[i]):
+                K.gemm(As[i], Bs[i], b_kn=True, tile=2, split_k=2, out=outs[i][r], workspace=wss[i][r])
+    torch.cuda.synchronize()
+    for i in range(2):
+        for r in range(8):
+            assert np.array_equal(host(outs[i][r]), want[i]), f'stream {i} launch {r}'
+
+
 @pytest.mark.parametrize('tile', [0, 1, 2, 4, 5, 9, 11, 13])
 @pytest.mark.parametrize('M,N,Kd,split', [(100, 200, 320, 1), (300, 136, 1024, 2), (100, 256, 384, 1),
                                           (300, 384, 1024, 4), (64, 128, 256, 2), (300, 192, 768, 1),
