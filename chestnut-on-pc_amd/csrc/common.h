@@ -91,6 +91,11 @@ __device__ __forceinline__ void store_sc1(__amdgpu_buffer_rsrc_t r, long off, ha
 __device__ __forceinline__ void store_sc1(__amdgpu_buffer_rsrc_t r, long off, half4_t v) {
   __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2_t, v), r, (int)off, 0, CPOL_SC1);
 }
+// The matching device-scope load: it observes every device-scope store that
+// has completed, on any CU.
+__device__ __forceinline__ float4_t load_sc1_f4(__amdgpu_buffer_rsrc_t r, long off) {
+  return __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, CPOL_SC1));
+}
 
 // ---------------------------------------------------------------------------
 // Wave64 reductions.  Lanes 0..63 of a CDNA wave form 4 DPP rows of 16.

@@ -23,7 +23,10 @@
 // MFMA 32x32x16 operand layout (lane l of 64): A row l%32, k = 8*(l/32)..+7;
 // B column l%32, same k; D element e of lane l is row 8*(e/4) + 4*(l/32) +
 // e%4, column l%32.  The layout is checked by the MFMA KAT (wmma.hip).
+#include <mutex>
 #include <type_traits>
+#include <utility>
+#include <vector>
 
 #include "common.h"
 #include "gemv_block.h"
@@ -33,6 +36,13 @@ namespace ck {
 namespace {
 
 constexpr int BK = 64;
+// LDS ring stages of the LDS-DMA kernel's two-K-group configurations, and
+// whether the f32 staging of both groups (8 regions of (BM/2) x (BN/2 + 8)
+// floats) fits in that ring.
+constexpr int dma_stages_kg2(int BM, int BN) {
+  return (BM == 64 && BN == 64) ? 4 : (6 * (BM + BN) * BK * 2 <= 163840 ? 6 : 4);
+}
+constexpr bool kg2_staging_fits(int BM, int BN, int S) { return 2 * 4 * (BM / 2) * (BN / 2 + 8) * 4 <= S * (BM + BN) * BK * 2; }
 constexpr int LDK = BK + 8;   // padded LDS row (halves)
 
 struct GemmParams {
@@ -54,6 +64,7 @@ struct GemmParams {
   int cc_log2, ch, cw, cwo;   // implicit conv: log2(channels), input height/width, output width
   const half_t* zero;         // implicit conv: 16 zero bytes
   int c_nm;                   // the split-K reduce stores element (m, n) at C[n*ldc + m]
+  unsigned* pair;             // split 2, f32 output: ticket counters of the in-kernel finish (null: a reduce follows)
 };
 
 // Implicit 3x3 stride-2 pad-1 convolution: the A chunk (8 halves) of patch
@@ -633,6 +644,55 @@ __device__ __forceinline__ void dma_issue_range(const half_t* const* asrc, const
 // 8 bytes per chunk, the fewest passes 512 bytes take.
 __device__ __forceinline__ int bt_swz(int row) { return ((row & 3) << 2) | ((row >> 3) & 1); }
 
+// Split-K in pairs (split 2, f32 output, p.pair set; the staged two-group
+// epilogue): the two waves that computed the same rows of a sub-tile over
+// the two halves of K finish them between them, with no reduce launch.  Each
+// has stored its partial rows with device-scope (sc1) stores; it waits until
+// they have completed, then takes a ticket, an atomic add on the rows'
+// counter.  Every launch adds exactly two to each counter it uses, so the
+// counters are even between launches and an odd ticket marks the second wave
+// of the pair.  That wave reads the other split's rows with device-scope
+// loads (the other wave's stores had completed before its ticket, which
+// this wave has seen) and writes C = (0 + own) + other (+ bias): the value the
+// reduce computes, (0 + p0) + p1 (+ bias), since a sum of two floats does not
+// depend on their order, the sign of a zero included.  No wave waits for
+// another.  own[i]: the wave's partial chunk i (row r0 + q / CPR, column
+// nw + 4 (q % CPR), q = lane + 64 i); tix: the rows' counter.
+template <int NQ, int HR, int CPR>
+__device__ __forceinline__ void pair_finish(const GemmParams& p, const float4_t (&own)[NQ], int r0, int nw, int sp,
+                                            int bz, int tix, int lane) {
+  asm volatile("" ::: "memory");
+  wait_vm_lgkm0<0>();   // this wave's partial stores have completed at device scope
+  asm volatile("" ::: "memory");
+  unsigned tk = 0;
+  if (lane == 0) tk = __hip_atomic_fetch_add(p.pair + tix, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  tk = __builtin_amdgcn_readfirstlane(tk);
+  asm volatile("" ::: "memory");
+  if ((tk & 1u) == 0) return;   // first of the pair: the other wave finishes these rows
+  const long MN = (long)p.M * p.N;
+  const __amdgpu_buffer_rsrc_t ro = sc1_rsrc(p.ws + ((long)(1 - sp) * p.batch + bz) * MN, 4 * MN);
+  float4_t o[NQ];
+#pragma unroll
+  for (int i = 0; i < NQ; ++i) {
+    const int q = lane + 64 * i, m = r0 + q / CPR, n = nw + (q % CPR) * 4;
+    o[i] = (m < p.M && n < p.N) ? load_sc1_f4(ro, ((long)m * p.N + n) * 4) : float4_t{0.f, 0.f, 0.f, 0.f};
+  }
+  float* C = static_cast<float*>(p.C) + bz * p.sC;
+  const float* bias = p.bias ? p.bias + bz * p.sBias : nullptr;
+#pragma unroll
+  for (int i = 0; i < NQ; ++i) {
+    const int q = lane + 64 * i, m = r0 + q / CPR, n = nw + (q % CPR) * 4;
+    if (m >= p.M || n >= p.N) continue;
+    float4_t v;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      v[e] = (0.f + own[i][e]) + o[i][e];
+      if (bias) v[e] += bias[n + e];
+    }
+    *reinterpret_cast<float4_t*>(C + (long)m * p.ldc + n) = v;
+  }
+}
+
 // The two K-groups' sum fused into the staged f32 epilogue (EPI_F32 and
 // EPI_PARTIALS on kernels with two K-groups of NWG waves): every wave stages
 // its group's sub-tile in a region of its own (group g, wave w: region
@@ -644,7 +704,7 @@ __device__ __forceinline__ int bt_swz(int row) { return ((row & 3) << 2) | ((row
 // retired (barrier); base: the LDS ring.
 template <int WM, int WN, int FM, int FN, int EPI, bool SWP, int NWG>
 __device__ __forceinline__ void store_staged_kg2(const GemmParams& p, const float16_t (&acc)[FM][FN], char* base,
-                                                 int grp, int w4, int mw, int nw, int sp, int bz, int lane) {
+                                                 int grp, int w4, int mw, int nw, int sp, int bz, int tile, int lane) {
   static_assert(EPI == EPI_F32 || EPI == EPI_PARTIALS, "f32 outputs only");
   constexpr int PF = WN + 8, REGION = WM * PF * 4, CPR = WN / 4;
   float* st = reinterpret_cast<float*>(base + (grp * NWG + w4) * REGION);
@@ -680,19 +740,25 @@ __device__ __forceinline__ void store_staged_kg2(const GemmParams& p, const floa
   const bool sc1 = sc1_ok(plane);
   const __amdgpu_buffer_rsrc_t rs = sc1_rsrc(dst, sc1 ? plane : 0);
   const float* bias = (!to_ws && p.bias) ? p.bias + bz * p.sBias : nullptr;
-  constexpr int HR = WM / 2;   // rows per wave
-#pragma unroll 4
-  for (int q = lane; q < HR * CPR; q += 64) {
-    const int r = grp * HR + q / CPR, c = (q % CPR) * 4;
+  constexpr int HR = WM / 2;             // rows per wave
+  constexpr int NQ = HR * CPR / 64;      // 16-byte chunks per lane
+  static_assert(NQ * 64 == HR * CPR, "chunks per lane");
+  float4_t own[NQ];
+#pragma unroll
+  for (int i = 0; i < NQ; ++i) {
+    const int q = lane + 64 * i, r = grp * HR + q / CPR, c = (q % CPR) * 4;
     const int m = mw + r, n = nw + c;
-    if (m >= p.M || n >= p.N) continue;
     float4_t v = *reinterpret_cast<const float4_t*>(s0 + r * PF + c) + *reinterpret_cast<const float4_t*>(s1 + r * PF + c);
+    own[i] = v;
+    if (m >= p.M || n >= p.N) continue;
     if (bias)
 #pragma unroll
       for (int e = 0; e < 4; ++e) v[e] += bias[n + e];
     if (sc1) store_sc1(rs, ((long)m * ld + n) * 4, v);
     else __builtin_nontemporal_store(v, reinterpret_cast<float4_t*>(dst + (long)m * ld + n));
   }
+  if constexpr (EPI == EPI_F32)
+    if (p.pair) pair_finish<NQ, HR, CPR>(p, own, mw + grp * HR, nw, sp, bz, (tile * NWG + w4) * 2 + grp, lane);
 }
 
 // KG K-groups of NWG waves each (64*NWG*KG threads): group g consumes
@@ -923,13 +989,13 @@ __global__ __launch_bounds__(64 * NWG * KG) void gemm_dma_kernel(const GemmParam
 
   // f32 outputs of two K-groups: the groups' sum inside the staged epilogue
   constexpr bool KG2_STAGED =
-      KG == 2 && (EPI == EPI_F32 || EPI == EPI_PARTIALS) && 2 * NWG * WM * (WN + 8) * 4 <= S * STAGE * 2;
+      KG == 2 && NWG == 4 && (EPI == EPI_F32 || EPI == EPI_PARTIALS) && kg2_staging_fits(BM, BN, S);
   if constexpr (KG2_STAGED) {
     if (p.vec) {
       wait_vm_lgkm0<0>();   // every wave is past its last ring read
       lds_barrier();
       store_staged_kg2<WM, WN, FM, FN, EPI, SWP, NWG>(p, acc, reinterpret_cast<char*>(lds), grp, w4, m0 + wm * WM,
-                                                      n0 + wn * WN, sp, bz, lane);
+                                                      n0 + wn * WN, sp, bz, (bz * p.Mt + mt) * p.Nt + nt, lane);
       return;
     }
   }
@@ -1199,7 +1265,7 @@ __global__ __launch_bounds__(512) void gemm_kn_rb_kernel(const GemmParams p) {
     wait_vm_lgkm0<0>();
     lds_barrier();
     store_staged_kg2<WM, WN, FM, FN, EPI_F32, true, NWG>(p, acc, reinterpret_cast<char*>(lds), grp, w4, m0 + wm * WM,
-                                                         n0 + wn * WN, sp, bz, lane);
+                                                         n0 + wn * WN, sp, bz, (bz * p.Mt + mt) * p.Nt + nt, lane);
     return;
   }
   // group 1 hands its partial tile to group 0 through LDS
@@ -1281,7 +1347,7 @@ void launch_dma_tile(const GemmParams& p, bool kg2, hipStream_t s) {
   const int grid = p.Mt * p.Nt * p.split * p.batch;
   constexpr int stage_bytes = (BM + BN) * BK * 2;
   constexpr int S1 = (5 * stage_bytes <= 163840) ? 5 : 4;
-  constexpr int S2 = (BM == 64 && BN == 64) ? 4 : (6 * stage_bytes <= 163840 ? 6 : 4);
+  constexpr int S2 = dma_stages_kg2(BM, BN);
   if (kg2) CK_LAUNCH((gemm_dma_kernel<BM, BN, S2, 2, EPI>), dim3(grid), dim3(512), 0, s, p);
   else CK_LAUNCH((gemm_dma_kernel<BM, BN, S1, 1, EPI>), dim3(grid), dim3(256), 0, s, p);
   CK_LAUNCHED("gemm_dma");
@@ -1293,7 +1359,7 @@ void launch_dma_tile_cv(const GemmParams& p, bool kg2, hipStream_t s) {
   const int grid = p.Mt * p.Nt * p.split * p.batch;
   constexpr int stage_bytes = (BM + BN) * BK * 2;
   constexpr int S1 = (5 * stage_bytes <= 163840) ? 5 : 4;
-  constexpr int S2 = (BM == 64 && BN == 64) ? 4 : (6 * stage_bytes <= 163840 ? 6 : 4);
+  constexpr int S2 = dma_stages_kg2(BM, BN);
   if (kg2) CK_LAUNCH((gemm_dma_kernel<BM, BN, S2, 2, EPI, 4, false, true>), dim3(grid), dim3(512), 0, s, p);
   else CK_LAUNCH((gemm_dma_kernel<BM, BN, S1, 1, EPI, 4, false, true>), dim3(grid), dim3(256), 0, s, p);
   CK_LAUNCHED("gemm_dma_conv");
@@ -1418,6 +1484,55 @@ bool bt_direct(const GemmDesc& d) {
   if (d.N % 128 != 0) return false;
   if (d.tile == 1) return (d.K / d.split) % (2 * BK) == 0;
   return d.tile == 9;   // 256x128, 8 waves in one K-group
+}
+
+// Ticket counters of the in-kernel split-2 finish (pair_finish): a static
+// per-device array, zero when the code object loads; every launch leaves the
+// counters it uses even.  Each stream gets a slot of its own on first use,
+// so split-2 GEMMs running at the same time on different streams never share
+// a counter; once every slot is taken, further streams get the reduce
+// launch.  A captured graph keeps the slot of the stream it was captured on:
+// replaying it on another stream while the capturing stream runs split-2
+// GEMMs races on that slot.
+constexpr int kPairSlots = 16;
+constexpr int kPairTickets = 8192;   // counters per slot
+constexpr int kPairDevices = 64;
+__device__ __align__(256) unsigned pair_tickets[kPairSlots * kPairTickets];
+
+std::mutex g_pair_mu;
+unsigned* g_pair_base[kPairDevices] = {};
+std::vector<std::pair<int, hipStream_t>> g_pair_slots;   // (device, stream), in order of first use
+
+// The ticket slot for a launch on stream s of the current device, or null
+// (no slot left, or the stream belongs to another device).
+unsigned* pair_slot(hipStream_t s) {
+  int dev = -1;
+  CK_HIP(hipGetDevice(&dev));
+  if (dev < 0 || dev >= kPairDevices) return nullptr;
+  if (s) {
+    hipDevice_t sdev = -1;
+    CK_HIP(hipStreamGetDevice(s, &sdev));
+    if (sdev != dev) return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_pair_mu);
+  if (!g_pair_base[dev]) {
+    void* q = nullptr;
+    CK_HIP(hipGetSymbolAddress(&q, HIP_SYMBOL(pair_tickets)));
+    CK_REQUIRE(q != nullptr, "gemm: split-K ticket array has no device address");
+    g_pair_base[dev] = static_cast<unsigned*>(q);
+  }
+  int slot = -1, used = 0;
+  for (const auto& e : g_pair_slots) {
+    if (e.first != dev) continue;
+    if (e.second == s) slot = used;
+    ++used;
+  }
+  if (slot < 0) {
+    if (used >= kPairSlots) return nullptr;
+    g_pair_slots.emplace_back(dev, s);
+    slot = used;
+  }
+  return g_pair_base[dev] + (size_t)slot * kPairTickets;
 }
 
 int tile_base(int tile) { const int c = tile % 10; return c > 4 ? c - 4 : c; }
@@ -1546,6 +1661,22 @@ void launch_gemm(GemmDesc d, hipStream_t s) {
     }
     p.vec = v ? 1 : 0;
   }
+  // Split 2 with an f32 output on a kernel with the two-group staged
+  // epilogue (the [K][N] register-B tile 2; [N][K] LDS-DMA tiles 1-4 with
+  // two K-groups whose staging fits the ring) finishes in the kernel
+  // (pair_finish) instead of a reduce launch.  Its partial planes must be
+  // addressable by 32-bit buffer offsets (device-scope stores and loads).
+  p.pair = nullptr;
+  {
+    const int bm = tile_bm(d.tile), bn = tile_bn(d.tile);
+    const bool staged = d.b_kn ? (d.tile == 2 && bt_direct(d))
+                               : (d.tile >= 1 && d.tile <= 4 && p.kps % (2 * BK) == 0 &&
+                                  kg2_staging_fits(bm, bn, dma_stages_kg2(bm, bn)));
+    const long tickets = (long)d.batch * p.Mt * p.Nt * 4 * 2;
+    if (staged && d.split == 2 && d.epi == EPI_F32 && p.vec && !conv && 4L * d.M * d.N < (1L << 31) &&
+        tickets <= kPairTickets)
+      p.pair = pair_slot(s);
+  }
   if (d.epi == EPI_QKV_FRAG) {
     const int dh = d.qk_cols / 2;
     const int wn = tile_bn(d.tile) / 2;   // columns per wave
@@ -1577,7 +1708,7 @@ void launch_gemm(GemmDesc d, hipStream_t s) {
     // reads cost more than the transpose pass saves (config 1: 44.6 against
     // 33.2 us; two K-groups 32.6 against 34.9 us).
     launch_dma_bt(p, d.tile, true, s);
-    if (d.split > 1) launch_reduce<EPI_F32>(p, s);
+    if (d.split > 1 && !p.pair) launch_reduce<EPI_F32>(p, s);
     return;
   }
   if (d.b_kn) {   // transpose B into the workspace tail, then the NT LDS-DMA kernel
@@ -1595,7 +1726,7 @@ void launch_gemm(GemmDesc d, hipStream_t s) {
     return;
   }
   switch (d.epi) {
-    case EPI_F32: launch_epi<false, EPI_F32>(d.tile, p, s); if (d.split > 1) launch_reduce<EPI_F32>(p, s); break;
+    case EPI_F32: launch_epi<false, EPI_F32>(d.tile, p, s); if (d.split > 1 && !p.pair) launch_reduce<EPI_F32>(p, s); break;
     case EPI_F16_BIAS: launch_epi<false, EPI_F16_BIAS>(d.tile, p, s); if (d.split > 1) launch_reduce<EPI_F16_BIAS>(p, s); break;
     case EPI_F16_BIAS_RELU: launch_epi<false, EPI_F16_BIAS_RELU>(d.tile, p, s); if (d.split > 1) launch_reduce<EPI_F16_BIAS_RELU>(p, s); break;
     case EPI_F16_BIAS_GELU: launch_epi<false, EPI_F16_BIAS_GELU>(d.tile, p, s); if (d.split > 1) launch_reduce<EPI_F16_BIAS_GELU>(p, s); break;
