@@ -196,6 +196,13 @@ int ck_gemv(const void* W, const float* x, const float* bias, float* y, int rows
  * workspace: split_k * M * N floats when split_k > 1, plus, for a [K][N] B
  * on tiles 1-8, N * K halves for B transposed to [N][K] (query with
  * ck_gemm_workspace, which also resolves auto tile/split).
+ * split_k = 2 on tile 2 ([K][N] B) or on tiles 2-4 ([N][K] B, K per split a
+ * multiple of 128) finishes inside the GEMM launch (no reduce launch): the
+ * result is bit for bit the reduce's.  It counts finished workgroups in a
+ * static per-device array with a slot per stream (16 streams per device;
+ * later streams get the reduce launch), so such calls may run at the same
+ * time on different streams; a graph captured with such a call keeps its
+ * capturing stream's slot and must not run while that stream runs one.
  * Replaces: launch of the WMMA GEMM kernels r_6_2 / r_2_24 / r_12_32_4 /
  * r_48_32_4 (bench_r62.py:13-29, bench_r12.py, bench_r48.py). */
 int ck_gemm_workspace(int M, int N, int K, int b_kn, int* tile, int* split_k, size_t* ws_bytes);
