@@ -97,6 +97,26 @@ __device__ __forceinline__ float4_t load_sc1_f4(__amdgpu_buffer_rsrc_t r, long o
   return __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, CPOL_SC1));
 }
 
+// LDS-DMA destination pointers, explicit memory waits and the raw barrier.
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// s_waitcnt vmcnt(N) lgkmcnt(0): at most N vector-memory operations of this
+// wave outstanding (they complete in issue order), no LDS operation.
+template <int N>
+__device__ __forceinline__ void wait_vm_lgkm0() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  // gfx9 s_waitcnt: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt_hi[15:14]
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (0x0 << 8) | (((N >> 4) & 0x3) << 14));
+}
+
+// s_barrier without __syncthreads' release fence (which would drain vmcnt to
+// zero on gfx9 and serialise prefetches that are still in flight).
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 // ---------------------------------------------------------------------------
 // Wave64 reductions.  Lanes 0..63 of a CDNA wave form 4 DPP rows of 16.
 // Inside a row: xor-1 and xor-2 exchanges (quad_perm), then the half-row and

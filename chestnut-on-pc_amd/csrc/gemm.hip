@@ -369,20 +369,6 @@ __global__ __launch_bounds__(256) void splitk_reduce_gemv_kernel(const GemmParam
 //   The barrier is the raw s_barrier: the release fence of __syncthreads
 //   would drain vmcnt to zero on gfx9 and serialise the prefetch.
 // ---------------------------------------------------------------------------
-typedef __attribute__((address_space(3))) void* lds_ptr_t;
-
-template <int N>
-__device__ __forceinline__ void wait_vm_lgkm0() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  // gfx9 s_waitcnt: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt_hi[15:14]
-  __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (0x0 << 8) | (((N >> 4) & 0x3) << 14));
-}
-
-__device__ __forceinline__ void lds_barrier() {
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-}
 
 // Issue one K-step's loads of this wave into LDS stage `st` (A rows then B rows).
 // ko: the K-step's offset in A (halves); bko: in B (ko for a [N][K] B, ko
