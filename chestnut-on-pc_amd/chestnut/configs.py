@@ -1,6 +1,6 @@
 """BASELINE configs 1-3 as stand-alone workloads for timing and rocprofv3.
 
-    python -m chestnut.configs --config 1|2|3|chain [--reps N] [--warmup-ms MS] [--out PATH]
+    python -m chestnut.configs --config 1|2|3|chain|frames39 [--reps N] [--warmup-ms MS] [--out PATH]
 
 Each run first copies 256 MiB device to device (the calibration dispatch the
 FETCH_SIZE / WRITE_SIZE summaries scale by), runs the config's kernels
@@ -24,6 +24,11 @@ counter passes.
      plain and as one graph; and frame-sized graphs (38 launches, the 39M
      frame's dispatch count) replayed 200 times, whose per-launch cost less
      the long chain's is the fixed cost of one graph launch
+  frames39  BASELINE config 4 frame by frame: the 39M engine's device-resident
+     frame (ck_frame_launch) 200 times as one graph launch each, then (after
+     one torch kernel that marks the switch in a kernel trace) 200 times as
+     plain launches; `python -m chestnut.profiling gaps` splits a kernel
+     trace of it into the two runs and reports where each frame's time goes
 """
 import argparse
 import json
@@ -181,9 +186,51 @@ def launch_chain(torch, reps=0, warmup_ms=0):
     return res
 
 
+def frames39(torch, reps=0, warmup_ms=300.0):
+    from . import spec as S
+    from .engine import Engine
+    sp = S.get_spec('driving_39m')
+    n = reps or 200
+    res = {'config': 'frames39', 'workload': 'driving_39m frames: graph replay, then plain launches',
+           'frames_per_mode': n, 'modes': ['graph', 'eager']}
+    with Engine(sp) as eng:
+        rng = np.random.default_rng(4)
+        eng.write('warped', rng.integers(0, 256, (2, 6, sp['img_h'], sp['img_w']), dtype=np.uint8))
+        p = np.zeros(sp['desire_len'] + 4 + sp['feat_len'], np.float32)
+        p[8:10] = (1.0, 0.0)
+        eng.write('packed', p)
+        res['plan'] = eng.plan()
+        t0 = time.perf_counter()
+        while time.perf_counter() - t0 < warmup_ms / 1e3:
+            for _ in range(50):
+                eng.frame_launch()
+            eng.synchronize()
+        for mode in res['modes']:
+            eng.set_graph(mode == 'graph')
+            eng.synchronize()
+            marker = torch.ones(16, device='cuda')
+            marker += 1                      # one torch kernel between the runs
+            torch.cuda.synchronize()
+            calls = []
+            t0 = time.perf_counter()
+            for _ in range(n):
+                c0 = time.perf_counter()
+                eng.frame_launch()
+                calls.append(time.perf_counter() - c0)
+            t1 = time.perf_counter()
+            eng.synchronize()
+            t2 = time.perf_counter()
+            res[f'{mode}_fps'] = round(n / (t2 - t0), 1)
+            # host side: one frame_launch call, and the launch loop per frame
+            # (a loop shorter than the frame period means the GPU bounds the rate)
+            res[f'{mode}_host_call_us'] = round(float(np.median(calls)) * 1e6, 1)
+            res[f'{mode}_host_loop_us_per_frame'] = round((t1 - t0) * 1e6 / n, 1)
+    return res
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(prog='python -m chestnut.configs')
-    ap.add_argument('--config', required=True, choices=('1', '2', '3', 'chain'))
+    ap.add_argument('--config', required=True, choices=('1', '2', '3', 'chain', 'frames39'))
     ap.add_argument('--reps', type=int, default=0, help='timed launches (default: 120 / 200 / 10)')
     ap.add_argument('--warmup-ms', type=float, default=300.0,
                     help='untimed repetitions for about this much GPU time before the timed ones')
@@ -196,6 +243,8 @@ def main(argv=None):
     t0 = time.perf_counter()
     if a.config == 'chain':
         res = launch_chain(torch)
+    elif a.config == 'frames39':
+        res = frames39(torch, a.reps, a.warmup_ms)
     else:
         cfg = int(a.config)
         reps = a.reps or {1: 120, 2: 200, 3: 10}[cfg]

@@ -8,6 +8,7 @@ Runs on the CPU over files a GPU run left behind:
     python -m chestnut.profiling frames TRACE.csv STATS.csv PLAN.json CMD > summary.md
     python -m chestnut.profiling traffic FETCH.csv WRITE.csv PMCRUN.json CMD OUT.json > summary.md
     python -m chestnut.profiling configs RUN.json TRACE.csv FETCH.csv WRITE.csv MFMA.csv CMD OUT.json > summary.md
+    python -m chestnut.profiling gaps RUN.json TRACE.csv CMD OUT.json [PLAIN_RUN.json] > summary.md
 
 PLAN.json is written by ``bench.py --dump-plan``; PMCRUN.json by
 ``bench.py --pmc-run FAMILY[,FAMILY...]``, which runs the first plan entry of
@@ -116,6 +117,103 @@ def frames_md(trace_csv, stats_csv, plan_json, cmd, top=16):
         n = n[:100] + '...' if len(n) > 100 else n
         out.append(f"| `{n}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.2f} | {float(r['MinNs']) / 1e3:.2f} | "
                    f"{float(r['MaxNs']) / 1e3:.2f} | {float(r['Percentage']):.2f} |")
+    return '\n'.join(out) + '\n'
+
+
+def load_trace_ts(path):
+    """(name, start ns, end ns) of every dispatch in start order."""
+    rows = list(csv.DictReader(open(path)))
+    rows.sort(key=lambda r: int(r['Start_Timestamp']))
+    return [(r['Kernel_Name'], int(r['Start_Timestamp']), int(r['End_Timestamp'])) for r in rows]
+
+
+def _frame_spans(seg, plan):
+    """Frames of the plan in a dispatch segment: (first start, last end, summed
+    kernel ns) of each, found as frames_from_trace finds them."""
+    trace = [(n, (e - s) / 1e3) for n, s, e in seg]
+    first = _expect(plan[0]['kernel'])
+    spans, i = [], 0
+    while i < len(seg):
+        if first not in seg[i][0]:
+            i += 1
+            continue
+        j, ok = i, True
+        for k, e in enumerate(plan):
+            tok = _expect(e['kernel'])
+            if j >= len(seg) or tok not in seg[j][0]:
+                ok = False
+                break
+            j += 1
+            if '+splitk' in e['kernel'] and 'partials' not in e['kernel'] and j < len(seg) \
+                    and 'splitk_reduce' in seg[j][0]:
+                j += 1
+            nxt = _expect(plan[k + 1]['kernel']) if k + 1 < len(plan) else None
+            while nxt != tok and j < len(seg) and tok in seg[j][0]:
+                j += 1
+        if ok:
+            spans.append((seg[i][1], seg[j - 1][2], sum(seg[x][2] - seg[x][1] for x in range(i, j)), j - i))
+            i = j
+        else:
+            i += 1
+    del trace
+    return spans
+
+
+def gaps(run_json, trace_csv):
+    """Split a kernel trace of `python -m chestnut.configs --config frames39`
+    at its two marker kernels (the only ones not from this library) into the
+    graph run and the plain-launch run, and per run report the frame period,
+    the span of a frame's kernels, their summed time, the idle time inside a
+    frame and the idle time between frames."""
+    run = json.load(open(run_json))
+    plan = run['plan']
+    tr = load_trace_ts(trace_csv)
+    marks = [i for i, r in enumerate(tr) if not _is_ck(r[0])]
+    groups = []   # index after each contiguous run of marker kernels
+    for i in marks:
+        if groups and i == groups[-1]:
+            groups[-1] = i + 1
+        else:
+            groups.append(i + 1)
+    starts = groups[-2:]
+    res = {'frames_per_mode': run['frames_per_mode']}
+    for mode, a, b in ((run['modes'][0], starts[0], None), (run['modes'][1], starts[1], None)):
+        end = len(tr) if mode == run['modes'][1] else next(i for i in marks if i >= a)
+        sp = _frame_spans(tr[a:end], plan)
+        if len(sp) < 3:
+            raise SystemExit(f'{mode}: fewer than 3 frames found')
+        per = [(sp[k + 1][0] - sp[k][0]) / 1e3 for k in range(len(sp) - 1)]
+        span = [(e - s) / 1e3 for s, e, _, _ in sp]
+        busy = [k / 1e3 for _, _, k, _ in sp]
+        bound = [(sp[k + 1][0] - sp[k][1]) / 1e3 for k in range(len(sp) - 1)]
+        res[mode] = {'frames': len(sp), 'dispatches_per_frame': sp[0][3], 'fps_wall': run.get(f'{mode}_fps'),
+                     'period_us': statistics.mean(per), 'span_us': statistics.mean(span),
+                     'kernel_us': statistics.mean(busy), 'idle_inside_us': statistics.mean(span) - statistics.mean(busy),
+                     'idle_between_us': statistics.mean(bound), 'idle_between_min_us': min(bound),
+                     'idle_between_max_us': max(bound)}
+    return res
+
+
+def gaps_md(res, cmd, plain=None):
+    out = ['Commands (run from the repository root on the MI355X box):', '', '```', cmd, '```', '']
+    if plain:
+        out += ['Untraced run: ' + '; '.join(
+            f"{m}: {plain[m + '_fps']} frames/s, host {plain.get(m + '_host_call_us')} us per frame_launch call, "
+            f"launch loop {plain.get(m + '_host_loop_us_per_frame')} us per frame" for m in plain['modes']) +
+            ' (the launch loop runs ahead of the GPU in both modes: the GPU bounds the frame rate).', '']
+    out += [
+           f"The 39M frame (BASELINE config 4) launched {res['frames_per_mode']} times back to back as one graph "
+           'launch per frame, then as plain launches (ck_set_graph(0)), inputs resident; frames found in the kernel '
+           'trace by matching the plan.  Period: start of a frame\'s first kernel to the next frame\'s; span: its '
+           'first kernel\'s start to its last kernel\'s end; kernel: the summed dispatch durations; idle inside: span '
+           'less kernel; idle between: last end of one frame to first start of the next.', '',
+           '| run | frames | dispatches/frame | fps (wall, this traced run) | period us | span us | kernel us | '
+           'idle inside us | idle between us (min / max) |', '|---|---:|---:|---:|---:|---:|---:|---:|---|']
+    for mode in ('graph', 'eager'):
+        r = res[mode]
+        out.append(f"| {mode} | {r['frames']} | {r['dispatches_per_frame']} | {r['fps_wall']} | {r['period_us']:.2f} | "
+                   f"{r['span_us']:.2f} | {r['kernel_us']:.2f} | {r['idle_inside_us']:.2f} | "
+                   f"{r['idle_between_us']:.2f} ({r['idle_between_min_us']:.2f} / {r['idle_between_max_us']:.2f}) |")
     return '\n'.join(out) + '\n'
 
 
@@ -338,6 +436,12 @@ def main(argv):
         with open(argv[5], 'w') as fh:
             json.dump(t, fh, indent=1)
         sys.stdout.write(traffic_md(t, argv[4]))
+    elif argv[0] == 'gaps':
+        res = gaps(argv[1], argv[2])
+        with open(argv[4], 'w') as fh:
+            json.dump(res, fh, indent=1)
+        plain = json.load(open(argv[5])) if len(argv) > 5 else None
+        sys.stdout.write(gaps_md(res, argv[3], plain))
     elif argv[0] == 'configs':
         # configs RUN.json TRACE.csv FETCH.csv WRITE.csv MFMA.csv CMD OUT.json [EXTRA.csv ...]
         # ('-' for a missing pass)

@@ -94,3 +94,47 @@ def test_traffic_calibration(tmp_path):
     d, a = t['entries']
     assert d['family'] == 'blk.down' and d['traffic_bytes'] == 100 * 1024 * 2 + 50 * 1024
     assert a['family'] == 'blk.attn' and a['read_bytes'] == 11 * 1024 * 2
+
+
+def _trace_ts_csv(path, seq):
+    """seq: (name, start us, end us)."""
+    with open(path, 'w', newline='') as fh:
+        w = csv.writer(fh)
+        w.writerow(['Kernel_Name', 'Start_Timestamp', 'End_Timestamp'])
+        for name, s, e in seq:
+            w.writerow([name, int(s * 1000), int(e * 1000)])
+
+
+def test_gaps_split_runs_at_markers(tmp_path):
+    """The frames39 trace: warm-up frames, a torch marker, graph frames, a
+    marker, plain-launch frames; per run the frame period, span, kernel time
+    and the idle time inside and between frames."""
+    plan = [{'name': 'inputs', 'kernel': 'gemv', 'flops': 0, 'bytes': 1},
+            {'name': 'decode', 'kernel': 'decode', 'flops': 0, 'bytes': 1}]
+    seq, t = [], 0.0
+
+    def frames(n, inside, between):
+        nonlocal t
+        for _ in range(n):
+            seq.append(('void ck::(anonymous namespace)::gemv_kernel<6>(args)', t, t + 3.0))
+            seq.append(('_ZN2ck12_GLOBAL__N_113decode_kernelEv', t + 3.0 + inside, t + 5.0 + inside))
+            t += 5.0 + inside + between
+    frames(2, 1.0, 1.0)                                   # warm-up
+    seq.append(('void at::native::fill_kernel(x)', t, t + 1.0)); t += 2.0
+    frames(4, 0.5, 6.0)                                   # graph
+    seq.append(('void at::native::fill_kernel(x)', t, t + 1.0))
+    seq.append(('void at::native::add_kernel(x)', t + 1.0, t + 2.0)); t += 3.0
+    frames(4, 2.0, 1.5)                                   # plain launches
+    _trace_ts_csv(tmp_path / 't.csv', seq)
+    run = {'frames_per_mode': 4, 'modes': ['graph', 'eager'], 'plan': plan, 'graph_fps': 1.0, 'eager_fps': 2.0}
+    with open(tmp_path / 'run.json', 'w') as fh:
+        json.dump(run, fh)
+    res = P.gaps(tmp_path / 'run.json', tmp_path / 't.csv')
+    g, e = res['graph'], res['eager']
+    assert g['frames'] == 4 and e['frames'] == 4 and g['dispatches_per_frame'] == 2
+    assert abs(g['kernel_us'] - 5.0) < 1e-9 and abs(e['kernel_us'] - 5.0) < 1e-9
+    assert abs(g['idle_inside_us'] - 0.5) < 1e-9 and abs(e['idle_inside_us'] - 2.0) < 1e-9
+    assert abs(g['idle_between_us'] - 6.0) < 1e-9 and abs(e['idle_between_us'] - 1.5) < 1e-9
+    assert abs(g['period_us'] - 11.5) < 1e-9 and abs(e['period_us'] - 8.5) < 1e-9
+    md = P.gaps_md(res, 'CMD', dict(run, graph_host_call_us=3.0, eager_host_call_us=4.0))
+    assert '| graph | 4 | 2 |' in md and 'host 3.0 us per frame_launch call' in md
