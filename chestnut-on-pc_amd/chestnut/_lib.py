@@ -64,6 +64,7 @@ _SIGS = {
     'ck_img_gather': (c_int, [c_void_p, c_int, c_int, c_int, c_int, c_void_p, c_int, c_void_p, c_void_p]),
     'ck_state_hashes': (c_int, [c_void_p, c_void_p, c_int]),
     'ck_time_launch_chain': (c_int, [c_int, c_int, c_int, c_int, P(c_float), c_void_p]),
+    'ck_time_operand_stream': (c_int, [c_int, c_int, c_int, c_int, c_int, c_int, P(c_float), c_void_p]),
     'ck_warp_nv12': (c_int, [c_void_p, c_void_p, c_size_t, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int,
                              c_int, c_int, c_void_p, c_void_p]),
     'ck_attention': (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_void_p]),

@@ -1,6 +1,6 @@
 """BASELINE configs 1-3 as stand-alone workloads for timing and rocprofv3.
 
-    python -m chestnut.configs --config 1|2|3|chain|frames39 [--reps N] [--warmup-ms MS] [--out PATH]
+    python -m chestnut.configs --config 1|2|3|chain|frames39|stream [--reps N] [--warmup-ms MS] [--out PATH]
 
 Each run first copies 256 MiB device to device (the calibration dispatch the
 FETCH_SIZE / WRITE_SIZE summaries scale by), runs the config's kernels
@@ -24,6 +24,12 @@ counter passes.
      plain and as one graph; and frame-sized graphs (38 launches, the 39M
      frame's dispatch count) replayed 200 times, whose per-launch cost less
      the long chain's is the fixed cost of one graph launch
+  stream  the block GEMM's operand stream without its arithmetic
+     (ck_time_operand_stream) on the MLP-up shape (512 x 8192 x 2048, 128x128
+     tiles): LDS-DMA with 4 and 8 waves and register loads, over 10 rotating
+     operand copies (weights from HBM, as in a frame) and over one (warm in
+     the Infinity Cache), beside the MLP-up GEMM itself (tile 5: 128x128, one
+     K-group, bias + GELU epilogue) over the same 10 copies
   frames39  BASELINE config 4 frame by frame: the 39M engine's device-resident
      frame (ck_frame_launch) 200 times as one graph launch each, then (after
      one torch kernel that marks the switch in a kernel trace) 200 times as
@@ -186,6 +192,38 @@ def launch_chain(torch, reps=0, warmup_ms=0):
     return res
 
 
+def operand_stream(torch, reps=0, warmup_ms=0):
+    import ctypes
+    from . import kernels as K
+    from ._lib import call
+    M, N, Kd = 512, 8192, 2048
+    n = reps or 200
+    res = {'config': 'stream', 'workload': 'MLP-up operand stream 512 x 8192 x 2048 (128x128 tiles, 64-wide K-steps)',
+           'shape': [M, N, Kd], 'bytes_per_launch_into_cus': 256 * (128 + 128) * Kd * 2, 'us_per_launch': {}}
+    names = {0: 'lds_dma_4_waves', 1: 'lds_dma_8_waves', 2: 'registers_4_waves'}
+    for copies in (10, 1):
+        for mode in (0, 1, 2):
+            v = ctypes.c_float()
+            call('ck_time_operand_stream', M, N, Kd, mode, copies, n, ctypes.byref(v), None)
+            res['us_per_launch'][f'{names[mode]}_copies{copies}'] = round(v.value, 2)
+    copies = 10
+    g = torch.Generator(device='cuda').manual_seed(3)
+    A = [(torch.randn(M, Kd, device='cuda', generator=g)).half() for _ in range(copies)]
+    W = [(torch.randn(N, Kd, device='cuda', generator=g) * 0.02).half() for _ in range(copies)]
+    b = torch.zeros(N, device='cuda')
+    out = torch.empty(M, N, device='cuda', dtype=torch.float16)
+    for r in range(n):
+        K.gemm_epi(A[r % copies], W[r % copies], b, 3, out, tile=5, split_k=1)
+    e0, e1 = _events(torch)
+    e0.record()
+    for r in range(n):
+        K.gemm_epi(A[r % copies], W[r % copies], b, 3, out, tile=5, split_k=1)
+    e1.record()
+    torch.cuda.synchronize()
+    res['us_per_launch']['gemm_mlp_up_tile5_copies10'] = round(e0.elapsed_time(e1) * 1e3 / n, 2)
+    return res
+
+
 def frames39(torch, reps=0, warmup_ms=300.0):
     from . import spec as S
     from .engine import Engine
@@ -230,7 +268,7 @@ def frames39(torch, reps=0, warmup_ms=300.0):
 
 def main(argv=None):
     ap = argparse.ArgumentParser(prog='python -m chestnut.configs')
-    ap.add_argument('--config', required=True, choices=('1', '2', '3', 'chain', 'frames39'))
+    ap.add_argument('--config', required=True, choices=('1', '2', '3', 'chain', 'frames39', 'stream'))
     ap.add_argument('--reps', type=int, default=0, help='timed launches (default: 120 / 200 / 10)')
     ap.add_argument('--warmup-ms', type=float, default=300.0,
                     help='untimed repetitions for about this much GPU time before the timed ones')
@@ -245,6 +283,8 @@ def main(argv=None):
         res = launch_chain(torch)
     elif a.config == 'frames39':
         res = frames39(torch, a.reps, a.warmup_ms)
+    elif a.config == 'stream':
+        res = operand_stream(torch, a.reps)
     else:
         cfg = int(a.config)
         reps = a.reps or {1: 120, 2: 200, 3: 10}[cfg]

@@ -245,6 +245,13 @@ int ck_time_launch_chain(int n_launches, int workgroups, int mode, int reps, flo
   CK_API_END
 }
 
+int ck_time_operand_stream(int M, int N, int K, int mode, int copies, int reps, float* us_per_launch, void* stream) {
+  CK_API_BEGIN
+  CK_REQUIRE(us_per_launch, "null argument");
+  *us_per_launch = time_operand_stream(M, N, K, mode, copies, reps, as_stream(stream));
+  CK_API_END
+}
+
 int ck_state_hashes(ck_engine* e, uint64_t* out, int n) {
   CK_API_BEGIN
   CK_REQUIRE(e && out, "null argument");

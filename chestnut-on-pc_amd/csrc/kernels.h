@@ -189,6 +189,10 @@ void launch_tokens(const half_t* stem_out, int n_spatial, int C5, half_t* F, hip
 // near-empty kernel on `workgroups` workgroups: mode 0 plain launches, mode 1
 // the chain captured once as a graph and replayed.  Synchronises s.
 float time_launch_chain(int n, int workgroups, int mode, int reps, hipStream_t s);
+// us per launch of the 128x128-tile GEMM operand stream without arithmetic
+// (mode 0: LDS-DMA ring, 4 waves; 1: the same with 8 waves; 2: register
+// loads), operands rotating over `copies` copies (stream.hip).
+float time_operand_stream(int M, int N, int K, int mode, int copies, int reps, hipStream_t s);
 
 // ---- content hash of device tensors (hash.hip) --------------------------------
 constexpr int HASH_SPAN_BYTES = 64 << 10;

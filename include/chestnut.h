@@ -173,6 +173,18 @@ int ck_state_hashes(ck_engine* e, uint64_t* out, int n);
  * ~0.5 ms per frame outside a CUDA graph, ~1.6 us per launch inside
  * (README.md:20-26, 73; NOTES.md:48-50). */
 int ck_time_launch_chain(int n_launches, int workgroups, int mode, int reps, float* us_per_launch, void* stream);
+
+/* The operand stream of a block GEMM (C = A B^T, A [M][K], B [N][K]) with its
+ * arithmetic taken out: the 128x128-tile grid, XCD-grouped tile order,
+ * 64-wide K-steps and per-step waits of the LDS-DMA GEMM, no MFMA, no
+ * fragment reads, no epilogue.  mode 0: LDS-DMA into a 4-stage ring, 4 waves;
+ * 1: the same with 8 waves; 2: 16-byte loads into registers, no LDS.  A and B
+ * rotate over `copies` copies (enough of them and B streams from HBM as the
+ * weights of a frame do); *us_per_launch: HIP events over `reps` launches
+ * after `reps` untimed ones.  M, N multiples of 128, K of 64.
+ * Replaces: the reference's per-kernel bench loop (bench_r62.py:25-37)
+ * applied to the GEMM's loads alone. */
+int ck_time_operand_stream(int M, int N, int K, int mode, int copies, int reps, float* us_per_launch, void* stream);
 int ck_read_tensor(ck_engine* e, const char* name, void* host, size_t nbytes);
 int ck_write_tensor(ck_engine* e, const char* name, const void* host, size_t nbytes);
 
