@@ -124,3 +124,14 @@ def test_engine_requires_library_no_fallback(monkeypatch, tmp_path):
     from chestnut import Engine
     with pytest.raises(RuntimeError, match='not built'):
         Engine('tiny')
+
+
+def test_operand_stream_rejects_bad_arguments():
+    """Argument checks run before any device call (so on the CPU too)."""
+    import ctypes
+    from chestnut._lib import call
+    v = ctypes.c_float()
+    for args, msg in (((256, 512, 320, 3, 1, 1), 'mode 0-2'), ((200, 512, 320, 0, 1, 1), 'multiples of 128'),
+                      ((256, 512, 100, 0, 1, 1), 'multiple of 64'), ((256, 512, 320, 0, 0, 1), 'copies')):
+        with pytest.raises(RuntimeError, match=msg):
+            call('ck_time_operand_stream', *args, ctypes.byref(v), None)

@@ -108,3 +108,15 @@ def test_fingerprint_diff_graph_eager_and_variant(gpu, tmp_path):
     r = probe.diff(base, var, ignore=('ws',))
     print(f'[probe] diff with blk0.up at tile 4 split 2: {r}', flush=True)
     assert r is not None and r['launch'] == 'blk0.up' and 'u' in r['tensors']
+
+
+def test_operand_stream_workload_runs(gpu):
+    """ck_time_operand_stream (the block GEMM's loads without arithmetic) runs
+    in all three modes on a small grid and reports a positive time per launch."""
+    import ctypes
+    from chestnut._lib import call
+    for mode in (0, 1, 2):
+        v = ctypes.c_float()
+        call('ck_time_operand_stream', 256, 512, 320, mode, 2, 3, ctypes.byref(v), None)
+        print(f'[stream] mode {mode}: {v.value:.2f} us per launch', flush=True)
+        assert v.value > 0
