@@ -376,11 +376,11 @@ def test_attention_vs_oracle(gpu, T, H, hd):
     assert np.max(np.abs(out - ref)) <= 2.0 ** -9 * np.max(np.abs(ref))
 
 
-@pytest.mark.parametrize('d', [128, 512, 2048])
-def test_layernorm_vs_oracle(gpu, d):
+@pytest.mark.parametrize('d,rows', [(128, 37), (512, 37), (2048, 37), (2048, 512), (1024, 1024)])
+def test_layernorm_vs_oracle(gpu, d, rows):
     from chestnut import kernels as K
-    rng = np.random.default_rng(d)
-    x = (rng.standard_normal((37, d)) * 2 + 0.5).astype(np.float32)
+    rng = np.random.default_rng(d + rows)
+    x = (rng.standard_normal((rows, d)) * 2 + 0.5).astype(np.float32)
     g = (1 + 0.1 * rng.standard_normal(d)).astype(np.float32)
     b = (0.1 * rng.standard_normal(d)).astype(np.float32)
     ref = OM.layernorm(x, g, b, 1e-5)
