@@ -385,11 +385,12 @@ def main():
                          'comma-separated FAMILY (or the entry of that exact name, e.g. blk1.ln1) alone '
                          '--pmc-reps times; writes --pmc-out and exits')
     ap.add_argument('--pmc-reps', type=int, default=10)
-    ap.add_argument('--pmc-out', default='gpurun_out/pmc_run.json')
+    ap.add_argument('--pmc-out', default='pmc_run.json')
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get('WORLD_SIZE', '1')) != 1:
         sys.exit('bench.py measures one GPU only: this build has no multi-GPU path '
-                 '(a recurrent batch-1 frame does not shard; see DESIGN.md). Run with --gpus 1.')
+                 '(a recurrent batch-1 frame runs on one GPU; more GPUs would serve more camera '
+                 'streams, one engine per GPU). Run with --gpus 1.')
 
     import torch
     assert torch.cuda.is_available(), 'bench.py needs a GPU'
