@@ -20,12 +20,15 @@
 //      (the QKV GEMM's fragment epilogue writes V that way);
 //   4. each wave leaves O_w, m_w and l_w in LDS; after one barrier the
 //      threads combine 4 features of one query at a time over the waves in
-//      fixed order: M = max m_w, O = sum 2^(m_w - M) O_w / sum 2^(m_w - M) l_w.
+//      fixed order: M = max m_w, O = sum 2^(m_w - M) O_w / sum 2^(m_w - M) l_w
+//      (with the O-projection: f16 P_w = O_w / l_w, weighted by 2^(m_w - M) l_w).
 // The result is deterministic; each wave streams only its own K and V.
 // Workgroups are regrouped by XCD (consecutive ids land on different XCDs):
 // each XCD's L2 then serves the K/V of T*hd*2*2 bytes for 2 heads.
 // MFMA 16x16x32 layout (lane l): A row l%16, k = 8*(l/16)..+7; B column
 // l%16, same k; D element i of lane l is row 4*(l/16)+i, column l%16.
+#include <type_traits>
+
 #include "common.h"
 #include "kernels.h"
 
@@ -77,9 +80,17 @@ __global__ __launch_bounds__(64 * att_waves(NKT)) void attention_kernel(const ha
   constexpr int KT = KPW / 16;       // 16-key tiles per wave
   constexpr int KB = KPW / 32;       // 32-key blocks (k-steps of P.V)
   constexpr int CT = HD / 16;        // 16-wide output tiles
-  constexpr int OP = HD + 4;         // partial-output row pitch (floats)
   static_assert(KPW % 32 == 0, "every wave must own whole 32-key blocks");
-  __shared__ __attribute__((aligned(16))) float part[WAVES][QB][OP];
+  // The waves' partial outputs: f16 P_w = O_w / l_w where the O-projection
+  // rides along (half the LDS bytes of the combine: 39M frame -0.75%), f32
+  // O_w otherwise (the f16 form's extra conversions cost the 1B frame +0.6%).
+  // Row pitch: f32 HD + 4 floats (the 4-row scatter of each lane's
+  // accumulators hits distinct banks); f16 HD + 8 halves (4 banks mod 64, so
+  // the 32 lanes of a half-wave writing 8 bytes each hit 64 distinct banks).
+  constexpr bool P16 = OTW > 0;
+  typedef std::conditional_t<P16, half_t, float> part_t;
+  constexpr int OP = P16 ? HD + 8 : HD + 4;
+  __shared__ __attribute__((aligned(16))) part_t part[WAVES][QB][OP];
   __shared__ float mrow[WAVES][QB], lrow[WAVES][QB];
   constexpr int KSO = HD / 32;       // k-steps of the O-projection
   constexpr int OBP = HD + 8;        // f16 output row pitch in LDS (16-byte rows)
@@ -152,6 +163,7 @@ __global__ __launch_bounds__(64 * att_waves(NKT)) void attention_kernel(const ha
 
   // ---- 2. wave-local softmax numerator per query (column r16 of q-tile qt) ----
   half8_t pa[KB][QT];
+  float lw[QT];
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
     float m = -INFINITY;
@@ -170,6 +182,7 @@ __global__ __launch_bounds__(64 * att_waves(NKT)) void attention_kernel(const ha
         pa[kb][qt][i] = (half_t)e;
       }
     acc = xor_sum(acc);
+    lw[qt] = acc;
     if (g == 0) {
       mrow[wave][qt * 16 + r16] = m;
       lrow[wave][qt * 16 + r16] = acc;
@@ -177,22 +190,40 @@ __global__ __launch_bounds__(64 * att_waves(NKT)) void attention_kernel(const ha
   }
 
   // ---- 3. O_w = e V over this wave's keys ----
-  float4_t o[QT][CT];
+  if constexpr (P16) {
+    // O_w^T = V^T e^T (operands swapped: lane (g, r16) ends with head dims
+    // 16ct + 4g .. +3 of query 16qt + r16), divided by the wave's l_w: a convex
+    // combination of V rows, so within V's range; one 8-byte write per tile
 #pragma unroll
-  for (int qt = 0; qt < QT; ++qt)
+    for (int qt = 0; qt < QT; ++qt) {
+      const float rl = 1.0f / lw[qt];
 #pragma unroll
-    for (int ct = 0; ct < CT; ++ct) {
-      float4_t a = {0.f, 0.f, 0.f, 0.f};
+      for (int ct = 0; ct < CT; ++ct) {
+        float4_t a = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int kb = 0; kb < KB; ++kb) a = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[kb][qt], vb[kb][ct], a, 0, 0, 0);
-      o[qt][ct] = a;
+        for (int kb = 0; kb < KB; ++kb) a = __builtin_amdgcn_mfma_f32_16x16x32_f16(vb[kb][ct], pa[kb][qt], a, 0, 0, 0);
+        *reinterpret_cast<half4_t*>(&part[wave][qt * 16 + r16][ct * 16 + 4 * g]) =
+            half4_t{(half_t)(a[0] * rl), (half_t)(a[1] * rl), (half_t)(a[2] * rl), (half_t)(a[3] * rl)};
+      }
     }
+  } else {
+    float4_t o[QT][CT];
 #pragma unroll
-  for (int qt = 0; qt < QT; ++qt)
+    for (int qt = 0; qt < QT; ++qt)
 #pragma unroll
-    for (int ct = 0; ct < CT; ++ct)
+      for (int ct = 0; ct < CT; ++ct) {
+        float4_t a = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int i = 0; i < 4; ++i) part[wave][qt * 16 + 4 * g + i][ct * 16 + r16] = o[qt][ct][i];
+        for (int kb = 0; kb < KB; ++kb) a = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[kb][qt], vb[kb][ct], a, 0, 0, 0);
+        o[qt][ct] = a;
+      }
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) part[wave][qt * 16 + 4 * g + i][ct * 16 + r16] = o[qt][ct][i];
+  }
   __syncthreads();
 
   // ---- 4. combine the waves: 4 features of one query per step, in fixed wave order ----
@@ -206,8 +237,15 @@ __global__ __launch_bounds__(64 * att_waves(NKT)) void attention_kernel(const ha
 #pragma unroll
     for (int w = 0; w < WAVES; ++w) {
       const float f = __builtin_amdgcn_exp2f(mrow[w][q] - M);
-      den += f * lrow[w][q];
-      acc += f * *reinterpret_cast<const float4_t*>(&part[w][q][c]);
+      if constexpr (P16) {
+        const float fl = f * lrow[w][q];
+        const half4_t pw = *reinterpret_cast<const half4_t*>(&part[w][q][c]);
+        den += fl;
+        acc += fl * float4_t{(float)pw[0], (float)pw[1], (float)pw[2], (float)pw[3]};
+      } else {
+        den += f * lrow[w][q];
+        acc += f * *reinterpret_cast<const float4_t*>(&part[w][q][c]);
+      }
     }
     const float rden = 1.0f / den;
     const half4_t v{(half_t)(acc[0] * rden), (half_t)(acc[1] * rden), (half_t)(acc[2] * rden), (half_t)(acc[3] * rden)};
