@@ -804,8 +804,12 @@ void ck_engine::upload(const std::string& name, const void* host, size_t nbytes)
 void ck_engine::drop_graph() {
   if (gexec) (void)hipGraphExecDestroy(gexec);
   if (graph) (void)hipGraphDestroy(graph);
+  if (gexec_io) (void)hipGraphExecDestroy(gexec_io);
+  if (graph_io) (void)hipGraphDestroy(graph_io);
   gexec = nullptr;
   graph = nullptr;
+  gexec_io = nullptr;
+  graph_io = nullptr;
   graph_nodes = 0;
 }
 
@@ -882,6 +886,32 @@ void ck_engine::capture() {
   }
 }
 
+// The same plan between the copies of run_frame: pinned staging -> warped and
+// packed, the plan, out -> pinned staging.  The staging addresses are fixed
+// for the engine's life, so the copy nodes are recorded once; each call
+// fills the staging before the launch and reads it after the sync.
+void ck_engine::capture_io() {
+  if (!gexec) capture();
+  CK_HIP(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal));
+  try {
+    CK_HIP(hipMemcpyAsync(ptr("warped"), h_warped, warped_bytes, hipMemcpyHostToDevice, stream));
+    CK_HIP(hipMemcpyAsync(ptr("packed"), h_packed, packed_len * sizeof(float), hipMemcpyHostToDevice, stream));
+    launch_plan();
+    CK_HIP(hipMemcpyAsync(h_out, ptr("out"), n_out * sizeof(float), hipMemcpyDeviceToHost, stream));
+  } catch (...) {
+    hipGraph_t g = nullptr;
+    (void)hipStreamEndCapture(stream, &g);
+    if (g) (void)hipGraphDestroy(g);
+    throw;
+  }
+  CK_HIP(hipStreamEndCapture(stream, &graph_io));
+  CK_HIP(hipGraphInstantiate(&gexec_io, graph_io, nullptr, nullptr, 0));
+  if (sp.graph_upload) {
+    CK_HIP(hipGraphUpload(gexec_io, stream));
+    CK_HIP(hipStreamSynchronize(stream));
+  }
+}
+
 void ck_engine::frame_launch() {
   if (use_graph) {
     if (!gexec) capture();
@@ -894,10 +924,15 @@ void ck_engine::frame_launch() {
 void ck_engine::run_frame(const uint8_t* warped, const float* packed, float* out) {
   std::memcpy(h_warped, warped, warped_bytes);
   std::memcpy(h_packed, packed, packed_len * sizeof(float));
-  CK_HIP(hipMemcpyAsync(ptr("warped"), h_warped, warped_bytes, hipMemcpyHostToDevice, stream));
-  CK_HIP(hipMemcpyAsync(ptr("packed"), h_packed, packed_len * sizeof(float), hipMemcpyHostToDevice, stream));
-  frame_launch();
-  CK_HIP(hipMemcpyAsync(h_out, ptr("out"), n_out * sizeof(float), hipMemcpyDeviceToHost, stream));
+  if (use_graph) {
+    if (!gexec_io) capture_io();
+    CK_HIP(hipGraphLaunch(gexec_io, stream));
+  } else {
+    CK_HIP(hipMemcpyAsync(ptr("warped"), h_warped, warped_bytes, hipMemcpyHostToDevice, stream));
+    CK_HIP(hipMemcpyAsync(ptr("packed"), h_packed, packed_len * sizeof(float), hipMemcpyHostToDevice, stream));
+    launch_plan();
+    CK_HIP(hipMemcpyAsync(h_out, ptr("out"), n_out * sizeof(float), hipMemcpyDeviceToHost, stream));
+  }
   CK_HIP(hipStreamSynchronize(stream));
   std::memcpy(out, h_out, n_out * sizeof(float));
 }

@@ -83,6 +83,10 @@ struct ck_engine {
   hipGraph_t graph = nullptr;
   hipGraphExec_t gexec = nullptr;
   size_t graph_nodes = 0;
+  // run_frame's graph: the input copies from the pinned staging, the plan and
+  // the output copy back, one launch per call (frame_launch replays `graph`)
+  hipGraph_t graph_io = nullptr;
+  hipGraphExec_t gexec_io = nullptr;
   float* ws = nullptr;
   size_t ws_floats = 0;
   // state hashing (ck_state_hashes): span table and per-span partials, built on first use
@@ -119,6 +123,7 @@ struct ck_engine {
   void launch_plan(const std::vector<char>* timed = nullptr,
                    std::vector<std::vector<std::pair<hipEvent_t, hipEvent_t>>>* events = nullptr);
   void capture();
+  void capture_io();
   void drop_graph();
   void reset_state();
   void run_range(int first, int last);
