@@ -607,6 +607,82 @@ __device__ __forceinline__ void store_staged(const GemmParams& p, const float16_
   }
 }
 
+// The QKV fragment epilogue for waves whose columns may straddle a head or
+// the Q/K/V boundaries (the 128x96 tile: one wave per 32 rows, 96 columns).
+// Each 32-column block of the wave is handled on its own; its kind (Q/K or
+// V), head and feature block are wave-uniform per block, and its chunks are
+// the ones store_staged writes for it: Q/K blocks are staged row-major
+// ([m][n], pitch WN + 8 halves) and V blocks transposed ([n][m], pitch
+// WM + 8) in two areas of the wave's LDS region.
+template <int WM, int WN, int FM, int FN>
+__device__ __forceinline__ void store_qkv_frag_blocks(const GemmParams& p, const float16_t (&acc)[FM][FN],
+                                                      const float (&bcol)[FN][1], char* region, int mw, int nw,
+                                                      int lane) {
+  constexpr int PH = WN + 8, PT = WM + 8;
+  half_t* sq = reinterpret_cast<half_t*>(region);   // [WM][PH]
+  half_t* sv = sq + WM * PH;                          // [WN][PT]
+#pragma unroll
+  for (int j = 0; j < FN; ++j) {
+    const int c = j * 32 + (lane & 31);
+    const float bv = bcol[j][0];
+    if (nw + j * 32 >= p.qk_cols) {
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int g4 = 0; g4 < 4; ++g4) {
+          half4_t h;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) h[e] = (half_t)(acc[i][j][4 * g4 + e] + bv);
+          *reinterpret_cast<half4_t*>(sv + c * PT + i * 32 + 8 * g4 + 4 * (lane >> 5)) = h;
+        }
+    } else {
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int e = 0; e < 16; ++e)
+          sq[(i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3)) * PH + c] = (half_t)(acc[i][j][e] + bv);
+    }
+  }
+  __builtin_amdgcn_wave_barrier();
+  asm volatile("" ::: "memory");
+  const int r = lane & 15, g = lane >> 4, hs = __builtin_ctz(p.head_dim), dh = p.qk_cols >> 1;
+  const auto rq = sc1_rsrc(p.C, 2L * p.M * p.qk_cols);
+  const auto rv = sc1_rsrc(p.vt, 2L * p.M * (p.N - p.qk_cols));
+#pragma unroll
+  for (int j = 0; j < FN; ++j) {
+    const int f = nw + j * 32;   // the block's first column
+    if (f >= p.N) continue;
+    if (f >= p.qk_cols) {
+      // V: per 32-token slice two blocks of 16 features x 32 tokens
+      const int f0 = f - p.qk_cols, h = f0 >> hs, c0 = f0 & (p.head_dim - 1);
+      const long cbase = (long)(h << (hs - 4)) + (c0 >> 4);
+      const int tpb = p.M >> 5;
+#pragma unroll
+      for (int blk = 0; blk < 2 * (WM / 32); ++blk) {
+        const int cb = blk & 1, tb = blk >> 1;
+        if (mw + tb * 32 >= p.M) continue;
+        const int nl = j * 32 + cb * 16 + r, ml = tb * 32 + g * 4;
+        const long chunk = ((cbase + cb) * tpb + (mw >> 5) + tb) * 64 + g * 16 + r;
+        const half4_t lo = *reinterpret_cast<const half4_t*>(sv + nl * PT + ml);
+        const half4_t hi = *reinterpret_cast<const half4_t*>(sv + nl * PT + ml + 16);
+        store_sc1(rv, chunk * 16, half8_t{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]});
+      }
+    } else {
+      // Q or K: blocks of 16 tokens x 32 features
+      const int which = f >= dh, f0 = f - which * dh, h = f0 >> hs, c0 = f0 & (p.head_dim - 1);
+      const long hbase = (long)(which * (dh >> hs) + h) * (p.M >> 4);   // 16-token blocks before this head
+      const int kpb = p.head_dim >> 5;
+#pragma unroll
+      for (int tb = 0; tb < WM / 16; ++tb) {
+        if (mw + tb * 16 >= p.M) continue;
+        const int ml = tb * 16 + r, nl = j * 32 + g * 8;
+        const long chunk = ((hbase + (mw >> 4) + tb) * kpb + (c0 >> 5)) * 64 + g * 16 + r;
+        store_sc1(rq, chunk * 16, *reinterpret_cast<const half8_t*>(sq + ml * PH + nl));
+      }
+    }
+  }
+}
+
 // Issue the load instructions [lo, hi) of a K-step (A rows first, then B
 // rows); lo and hi are compile-time after unrolling, so the untaken ones vanish.
 template <int NIA, int NIB, int STAGE_A, int BPOL = 0>
@@ -766,8 +842,13 @@ __device__ __forceinline__ void store_staged_kg2(const GemmParams& p, const floa
 // epilogue take this form.
 // CV: A is an implicit convolution (conv_a_src): the A chunk addresses are
 // recomputed for every K-step instead of advancing by the step.
-template <int BM, int BN, int S, int KG, int EPI, int NWG = 4, bool BT = false, bool CV = false>
+// WCOL: waves across the tile's columns.  2 (every tile but one): a group's
+// waves form an (NWG/2) x 2 grid.  1: the 128x96 QKV tile, one wave per 32
+// rows over all 96 columns (store_qkv_frag_blocks).
+template <int BM, int BN, int S, int KG, int EPI, int NWG = 4, bool BT = false, bool CV = false, int WCOL = 2>
 __global__ __launch_bounds__(64 * NWG * KG) void gemm_dma_kernel(const GemmParams p) {
+  static_assert(WCOL == 2 || (WCOL == 1 && EPI == EPI_QKV_FRAG && KG == 1 && !BT && !CV),
+                "one wave column: the QKV fragment epilogue on one K-group only");
   constexpr int STAGE_A = BM * BK, STAGE_B = BN * BK, STAGE = STAGE_A + STAGE_B;   // halves
   static_assert(S % KG == 0 && S / KG >= 2, "each K-group owns at least two ring stages");
   static_assert(KG == 1 || NWG == 4, "K-groups are built from 4-wave groups");
@@ -782,8 +863,9 @@ __global__ __launch_bounds__(64 * NWG * KG) void gemm_dma_kernel(const GemmParam
   // bank conflicts, of which it has fewer.)
   constexpr int BPOL = BM >= 128 ? 2 : 0;
   __shared__ __attribute__((aligned(1024))) half_t lds[S * STAGE];
-  constexpr int WM = BM / (NWG / 2), WN = BN / 2;
+  constexpr int WM = BM / (NWG / WCOL), WN = BN / WCOL;
   constexpr int FM = WM / 32, FN = WN / 32;
+  static_assert(FM * 32 == WM && FN * 32 == WN, "wave sub-tiles of whole 32x32 products");
   constexpr int NIA = BM / (8 * NWG), NIB = BN / (8 * NWG);   // load instructions per wave per step
   constexpr int NI = NIA + NIB;
   static_assert(NIA * 8 * NWG == BM && NIB * 8 * NWG == BN, "tile rows must split into whole load instructions");
@@ -791,7 +873,7 @@ __global__ __launch_bounds__(64 * NWG * KG) void gemm_dma_kernel(const GemmParam
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int grp = wave / NWG, w4 = wave % NWG;
-  const int wm = w4 >> 1, wn = w4 & 1;
+  const int wm = w4 / WCOL, wn = w4 % WCOL;
 
   const int total = p.Mt * p.Nt * p.split * p.batch;
   int L = blockIdx.x;
@@ -1018,10 +1100,16 @@ __global__ __launch_bounds__(64 * NWG * KG) void gemm_dma_kernel(const GemmParam
   }
 
   if (p.vec) {
-    constexpr int REGION = WM * (WN + 8) * 4;   // bytes per wave; the f32 staging is the largest
+    // bytes per wave: the f32 staging is the largest, or for one wave column
+    // the row-major Q/K area and the transposed V area side by side
+    constexpr int REGION = WCOL == 1 ? 2 * (WM * (WN + 8) + WN * (WM + 8)) : WM * (WN + 8) * 4;
     static_assert(NWG * REGION <= S * STAGE * 2, "LDS ring too small for the staged epilogue");
-    store_staged<WM, WN, FM, FN, EPI, SWP, NBC>(p, acc, bcol, reinterpret_cast<char*>(lds) + w4 * REGION, m0 + wm * WM,
-                                      n0 + wn * WN, sp, bz, lane);
+    if constexpr (WCOL == 1)
+      store_qkv_frag_blocks<WM, WN, FM, FN>(p, acc, bcol, reinterpret_cast<char*>(lds) + w4 * REGION, m0 + wm * WM,
+                                            n0 + wn * WN, lane);
+    else
+      store_staged<WM, WN, FM, FN, EPI, SWP, NBC>(p, acc, bcol, reinterpret_cast<char*>(lds) + w4 * REGION,
+                                                  m0 + wm * WM, n0 + wn * WN, sp, bz, lane);
     return;
   }
 
@@ -1398,6 +1486,14 @@ void launch_tile(const GemmParams& p, hipStream_t s) {
 template <bool BKN, int EPI>
 void launch_epi(int tile, const GemmParams& p, hipStream_t s) {
   const int c = tile % 10;
+  if (tile == 10) {   // 128x96, one wave column, 5-stage ring (5 x 28 KB): the QKV fragment epilogue only
+    if constexpr (!BKN && EPI == EPI_QKV_FRAG) {
+      CK_LAUNCH((gemm_dma_kernel<128, 96, 5, 1, EPI, 4, false, false, 1>), dim3(p.Mt * p.Nt), dim3(256), 0, s, p);
+      CK_LAUNCHED("gemm_dma");
+      return;
+    }
+    throw Error("gemm: tile 10 (128x96) serves the QKV fragment epilogue only");
+  }
   if (!BKN && tile == 9) {
     launch_dma_tile8<EPI>(p, s);
     return;
@@ -1522,9 +1618,13 @@ unsigned* pair_slot(hipStream_t s) {
 }
 
 int tile_base(int tile) { const int c = tile % 10; return c > 4 ? c - 4 : c; }
-bool tile_dma(int tile) { return tile <= 9; }
-int tile_bm(int tile) { return tile == 9 ? 256 : (tile_base(tile) == 1 || tile_base(tile) == 2) ? 128 : 64; }
-int tile_bn(int tile) { return tile == 9 ? 128 : (tile_base(tile) == 1 || tile_base(tile) == 3) ? 128 : 64; }
+bool tile_dma(int tile) { return tile <= 10; }
+int tile_bm(int tile) {
+  return tile == 9 ? 256 : tile == 10 ? 128 : (tile_base(tile) == 1 || tile_base(tile) == 2) ? 128 : 64;
+}
+int tile_bn(int tile) {
+  return tile == 9 ? 128 : tile == 10 ? 96 : (tile_base(tile) == 1 || tile_base(tile) == 3) ? 128 : 64;
+}
 
 }  // namespace
 
@@ -1553,7 +1653,9 @@ size_t gemm_plan(GemmDesc& d) {
     if (t < 64) bm = bn = 64;
     d.tile = bm == 128 ? (bn == 128 ? 1 : 2) : (bn == 128 ? 3 : 4);
   }
-  CK_REQUIRE((d.tile >= 1 && d.tile <= 9) || (d.tile >= 11 && d.tile <= 14), "gemm: unknown tile code");
+  CK_REQUIRE((d.tile >= 1 && d.tile <= 14), "gemm: unknown tile code");
+  CK_REQUIRE(d.tile != 10 || (d.epi == EPI_QKV_FRAG && !d.b_kn && d.conv_c == 0),
+             "gemm: tile 10 (128x96) serves the QKV fragment epilogue only");
   if (d.b_kn && !tile_dma(d.tile))
     CK_REQUIRE(d.tile == 11 || d.tile == 13, "gemm: [K][N] B on the register-staged kernel needs a 128-wide N tile");
   const long tiles = (long)ceil_div(d.M, tile_bm(d.tile)) * ceil_div(d.N, tile_bn(d.tile)) * d.batch;
@@ -1642,8 +1744,10 @@ void launch_gemm(GemmDesc d, hipStream_t s) {
     } else {
       const int el = (d.epi == EPI_F32 || d.epi == EPI_F32_RESID || d.epi == EPI_EMBED) ? 4 : 8;
       v = v && al16(d.C) && d.ldc % el == 0 && d.sC % el == 0;
+      // (the 128x96 tile's epilogue takes the Q/K/V boundary per 32-column block)
       if (d.epi == EPI_QKV || d.epi == EPI_QKV_FRAG)
-        v = v && d.qk_cols % tile_bn(d.tile) == 0 && d.M % 8 == 0 && d.vt_ld % 8 == 0 && al16(d.vt);
+        v = v && d.qk_cols % (d.tile == 10 ? 32 : tile_bn(d.tile)) == 0 && d.M % 8 == 0 && d.vt_ld % 8 == 0 &&
+            al16(d.vt);
     }
     p.vec = v ? 1 : 0;
   }
@@ -1665,7 +1769,9 @@ void launch_gemm(GemmDesc d, hipStream_t s) {
   }
   if (d.epi == EPI_QKV_FRAG) {
     const int dh = d.qk_cols / 2;
-    const int wn = tile_bn(d.tile) / 2;   // columns per wave
+    // columns a wave's epilogue keeps within one head: its sub-tile's, or on
+    // the 128x96 tile each 32-column block's
+    const int wn = d.tile == 10 ? 32 : tile_bn(d.tile) / 2;
     CK_REQUIRE(d.head_dim >= wn && (d.head_dim & (d.head_dim - 1)) == 0 && d.qk_cols % 2 == 0 &&
                    dh % d.head_dim == 0 && d.N == 3 * dh && d.M % 32 == 0 && d.N % tile_bn(d.tile) == 0,
                "gemm: QKV fragment epilogue needs N = 3d, d % head_dim == 0, head_dim a power of two no smaller "

@@ -7,7 +7,7 @@ def test_candidates_respect_epilogue_and_grid():
     sh = TU.shapes(S.get_spec('big_driving_1b'))
     M, N, K, kind, _ = sh['qkv']
     c = TU.candidates(M, N, K, kind)
-    assert (5, 1) in c and (1, 1) in c
+    assert (5, 1) in c and (1, 1) in c and (10, 1) in c                   # 10: the 128x96 QKV tile
     assert all(s == 1 for _, s in c) and all(t != 9 for t, _ in c)       # fragment epilogue: split 1, no 256-row tile
     M, N, K, kind, _ = sh['o']
     c = TU.candidates(M, N, K, kind)
@@ -17,6 +17,7 @@ def test_candidates_respect_epilogue_and_grid():
         bm, bn = TU.TILES[t]
         grid = -(-M // bm) * -(-N // bn) * s
         assert 64 <= grid <= 1024 and K % (64 * s) == 0
+    assert all(t != 10 for t, _ in c)                                      # 128x96 serves the QKV epilogue only
     M, N, K, kind, _ = sh['up']
     assert all(s == 1 for _, s in TU.candidates(M, N, K, kind))            # GELU epilogue is not split
 
