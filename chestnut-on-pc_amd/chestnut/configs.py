@@ -221,6 +221,13 @@ def operand_stream(torch, reps=0, warmup_ms=0):
     e1.record()
     torch.cuda.synchronize()
     res['us_per_launch']['gemm_mlp_up_tile5_copies10'] = round(e0.elapsed_time(e1) * 1e3 / n, 2)
+    # the QKV shape (N = 6144): 128x128 tiles (192 workgroups) against 128x96 (256), 12 copies of 27 MB
+    Nq = 6144
+    res['qkv'] = {'shape': [M, Nq, Kd], 'us_per_launch': {}}
+    for mode, tile, wgs in ((0, '128x128', 192), (3, '128x96', 256)):
+        v = ctypes.c_float()
+        call('ck_time_operand_stream', M, Nq, Kd, mode, 12, n, ctypes.byref(v), None)
+        res['qkv']['us_per_launch'][f'{tile}_{wgs}_workgroups_copies12'] = round(v.value, 2)
     return res
 
 

@@ -178,10 +178,11 @@ int ck_time_launch_chain(int n_launches, int workgroups, int mode, int reps, flo
  * arithmetic taken out: the 128x128-tile grid, XCD-grouped tile order,
  * 64-wide K-steps and per-step waits of the LDS-DMA GEMM, no MFMA, no
  * fragment reads, no epilogue.  mode 0: LDS-DMA into a 4-stage ring, 4 waves;
- * 1: the same with 8 waves; 2: 16-byte loads into registers, no LDS.  A and B
- * rotate over `copies` copies (enough of them and B streams from HBM as the
- * weights of a frame do); *us_per_launch: HIP events over `reps` launches
- * after `reps` untimed ones.  M, N multiples of 128, K of 64.
+ * 1: the same with 8 waves; 2: 16-byte loads into registers, no LDS; 3: mode 0
+ * on 128x96 tiles (the QKV GEMM's).  A and B rotate over `copies` copies
+ * (enough of them and B streams from HBM as the weights of a frame do);
+ * *us_per_launch: HIP events over `reps` launches after `reps` untimed ones.
+ * M a multiple of 128, N of the tile width (128, or 96 in mode 3), K of 64.
  * Replaces: the reference's per-kernel bench loop (bench_r62.py:25-37)
  * applied to the GEMM's loads alone. */
 int ck_time_operand_stream(int M, int N, int K, int mode, int copies, int reps, float* us_per_launch, void* stream);

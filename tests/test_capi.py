@@ -131,7 +131,8 @@ def test_operand_stream_rejects_bad_arguments():
     import ctypes
     from chestnut._lib import call
     v = ctypes.c_float()
-    for args, msg in (((256, 512, 320, 3, 1, 1), 'mode 0-2'), ((200, 512, 320, 0, 1, 1), 'multiples of 128'),
-                      ((256, 512, 100, 0, 1, 1), 'multiple of 64'), ((256, 512, 320, 0, 0, 1), 'copies')):
+    for args, msg in (((256, 512, 320, 4, 1, 1), 'mode 0-3'), ((200, 512, 320, 0, 1, 1), 'multiple of 128'),
+                      ((256, 512, 100, 0, 1, 1), 'K of 64'), ((256, 512, 320, 0, 0, 1), 'copies'),
+                      ((256, 512, 320, 3, 1, 1), 'tile width')):
         with pytest.raises(RuntimeError, match=msg):
             call('ck_time_operand_stream', *args, ctypes.byref(v), None)

@@ -112,11 +112,11 @@ def test_fingerprint_diff_graph_eager_and_variant(gpu, tmp_path):
 
 def test_operand_stream_workload_runs(gpu):
     """ck_time_operand_stream (the block GEMM's loads without arithmetic) runs
-    in all three modes on a small grid and reports a positive time per launch."""
+    in all four modes on a small grid and reports a positive time per launch."""
     import ctypes
     from chestnut._lib import call
-    for mode in (0, 1, 2):
+    for mode in (0, 1, 2, 3):
         v = ctypes.c_float()
-        call('ck_time_operand_stream', 256, 512, 320, mode, 2, 3, ctypes.byref(v), None)
+        call('ck_time_operand_stream', 256, 576 if mode == 3 else 512, 320, mode, 2, 3, ctypes.byref(v), None)
         print(f'[stream] mode {mode}: {v.value:.2f} us per launch', flush=True)
         assert v.value > 0
