@@ -5,11 +5,12 @@
 // Those kernels are serial K loops whose whole output tile lives in the
 // register file as loop-carried fragments, one block per SM (255 registers).
 // This file has two kernels instead:
-//   * gemm_dma_kernel (the production path, tile codes 1-9): A and B tiles go
+//   * gemm_dma_kernel (the production path, tile codes 1-10): A and B tiles go
 //     straight from global memory into an S-stage LDS ring with
 //     global_load_lds_dwordx4, XOR-swizzled for conflict-free MFMA operand
-//     reads; v_mfma_f32_32x32x16_f16 on a grid of 64x64 wave tiles; one or two
-//     K-groups; an LDS-staged epilogue (described at the kernel);
+//     reads; v_mfma_f32_32x32x16_f16 on a grid of 64x64 wave tiles (32x96 on
+//     the 128x96 QKV tile); one or two K-groups; an LDS-staged epilogue
+//     (described at the kernel);
 //   * gemm_kernel (tile codes 11-14): register-staged loads with rows padded
 //     to 72 halves, kept for a B operand given as [K][N], which it transposes
 //     in registers.
@@ -404,7 +405,8 @@ __device__ __forceinline__ void dma_issue(const half_t* const* asrc, const half_
 // 32-bit buffer offset (sc1_ok), and with non-temporal stores otherwise.
 // Requires (checked on the host, else the direct per-element stores run):
 // N % 8 == 0, ldc / batch stride / base of C and ws 16-byte compatible,
-// and for QKV qk_cols % BN == 0, M % 8 == 0 and vt_ld % 8 == 0.
+// and for QKV qk_cols % BN == 0 (% 32 on the 128x96 tile), M % 8 == 0 and
+// vt_ld % 8 == 0.
 //
 // EPI_QKV_FRAG writes the attention kernel's MFMA operands directly, in
 // 16-byte chunks ordered so that one wave's fragment load is one contiguous
