@@ -29,7 +29,7 @@ FAMILIES = ('qkv', 'o', 'up', 'down')        # per-block GEMMs (every layer gets
 SINGLE = ('stem0', 'stem1', 'stem2', 'stem3', 'stem4', 'embed')   # once-per-frame GEMMs
 # tile code -> (rows, columns) of the output tile (the codes of ck_gemm)
 TILES = {1: (128, 128), 2: (128, 64), 3: (64, 128), 4: (64, 64), 5: (128, 128), 6: (128, 64), 7: (64, 128),
-         8: (64, 64), 9: (256, 128), 10: (128, 96)}
+         8: (64, 64), 9: (256, 128), 10: (128, 96), 15: (32, 64)}
 
 
 def shapes(sp):
@@ -72,6 +72,8 @@ def candidates(M, N, K, kind, batch=1, min_wg=64, max_wg=1024):
         if t == 9 and kind in ('frag', 'conv'):
             continue
         if t == 10 and kind != 'frag':   # the 128x96 tile serves the QKV fragment epilogue only
+            continue
+        if t == 15 and kind == 'conv':   # the 32x64 tile has no implicit-conv A path
             continue
         for s in range(1, 17):
             if s > 1 and kind not in ('partials', 'reduce', 'conv'):

@@ -657,14 +657,13 @@ void ck_engine::build_plan() {
   // follows each of them adds partials + bias into x before normalising.
   // Tiles and splits were chosen on whole frames of the 1B model (a GEMM's
   // time inside the frame differs from its time in a loop of its own):
-  //   QKV, MLP up: 128x128, one K-group;  O-proj: 64x128, two K-groups,
-  //   split to fill 256 workgroups (128x64 until the cache-policy changes of
-  //   the stores and weight loads; retuned: -1.5% of the 1B frame);  MLP
-  //   down: 128x128, one K-group, split to fill 256.
+  //   QKV: 128x96 (below), MLP up: 128x128, one K-group;  O-proj: 64x128,
+  //   two K-groups, split to fill 256 workgroups (128x64 until the
+  //   cache-policy changes of the stores and weight loads; retuned: -1.5% of
+  //   the 1B frame);  MLP down: 128x128, one K-group, split to fill 256.
   //   GEMMs whose 128x128 tiles would leave most CUs idle (fewer than 64
-  //   tiles: the 39M model's 256 tokens x d = 512) run on 64x64 tiles with
-  //   one K-group, the residual ones split down to 4 K-steps per workgroup
-  //   (whole 39M frames: 0.264 -> 0.209 ms).
+  //   tiles: the 39M model's 256 tokens x d = 512) run on smaller tiles
+  //   (below; whole 39M frames on 64x64 tiles: 0.264 -> 0.209 ms).
   auto small = [&](int N) { return (long)ceil_div(T, 128) * ceil_div(N, 128) < 64; };
   auto resid_split = [&](int M, int N, int K, int bm, int bn, int kmult, int kmin) {
     const long tiles = (long)ceil_div(M, bm) * ceil_div(N, bn);
@@ -677,10 +676,16 @@ void ck_engine::build_plan() {
   // the bytes (1B: 192 -> 256 workgroups, QKV 22.96 -> 21.44 us, frame -1.9%)
   const long qt128 = (long)(T / 128) * (3 * d / 128), qt96 = (long)(T / 128) * (3 * d / 96);
   const bool qkv96 = T % 128 == 0 && (3 * d) % 96 == 0 && qt128 < 256 && qt96 <= 256 && sp.head_dim >= 32;
-  const int tile_o = small(d) ? 8 : 3, tile_dn = small(d) ? 8 : 5;
-  const int tile_qkv = small(3 * d) ? 8 : qkv96 ? 10 : 5, tile_up = small(F) ? 8 : 5;
+  // Small models: QKV and MLP-up on 32x64 tiles (gemm tile 15, two waves)
+  // where that grid still fits one wave of 256 workgroups, MLP-down on 64x64
+  // tiles with two K-groups, split to 512-wide K slices (39M frames, one
+  // process, alternating engines: 0.1866 -> 0.1816 ms; each alone less).
+  auto fits32 = [&](int N) { return (long)ceil_div(T, 32) * ceil_div(N, 64) <= 256; };
+  const int tile_o = small(d) ? 8 : 3, tile_dn = small(d) ? 4 : 5;
+  const int tile_qkv = small(3 * d) ? (fits32(3 * d) && sp.head_dim >= 32 ? 15 : 8) : qkv96 ? 10 : 5;
+  const int tile_up = small(F) ? (fits32(F) ? 15 : 8) : 5;
   const int s_o = small(d) ? resid_split(T, d, d, 64, 64, 64, 256) : resid_split(T, d, d, 64, 128, 128, 512);
-  const int s_dn = small(d) ? resid_split(T, d, F, 64, 64, 64, 256) : resid_split(T, d, F, 128, 128, 128, 512);
+  const int s_dn = small(d) ? resid_split(T, d, F, 64, 64, 128, 512) : resid_split(T, d, F, 128, 128, 128, 512);
   ck_engine* self = this;
   const long part_stride = (long)T * d;
   // attention + O-projection in one launch: one partial plane per head
@@ -714,7 +719,7 @@ void ck_engine::build_plan() {
     q.A = hb; q.lda = d; q.B = h16(p + "qkv.w"); q.ldb = d; q.C = ptr("qk"); q.ldc = 2 * d;
     q.bias = f32(p + "qkv.b"); q.M = T; q.N = 3 * d; q.K = d; q.epi = EPI_QKV_FRAG;
     q.vt = h16("vt"); q.qk_cols = 2 * d; q.vt_ld = T; q.head_dim = sp.head_dim;
-    q.tile = tile_qkv; q.split = 1;   // 128x96 or 128x128 tiles (64x64 when small), one K-group
+    q.tile = tile_qkv; q.split = 1;   // 128x96 or 128x128 tiles (32x64 or 64x64 when small), one K-group
     add_gemm(b + "qkv", "gemm_qkv", q);
     const half_t* qk = h16("qk");
     const half_t* vt = h16("vt");
@@ -742,7 +747,7 @@ void ck_engine::build_plan() {
     GemmDesc up;
     up.A = hb; up.lda = d; up.B = h16(p + "up.w"); up.ldb = d; up.C = ptr("u"); up.ldc = F;
     up.bias = f32(p + "up.b"); up.M = T; up.N = F; up.K = d; up.epi = EPI_F16_BIAS_GELU;
-    up.tile = tile_up; up.split = 1;  // 128x128 tiles (64x64 when small), one K-group, 5-stage ring
+    up.tile = tile_up; up.split = 1;  // 128x128 tiles (32x64 or 64x64 when small), one K-group
     add_gemm(b + "up", "gemm_gelu", up);
     GemmDesc dn;
     dn.A = h16("u"); dn.lda = F; dn.B = h16(p + "down.w"); dn.ldb = F;

@@ -1484,7 +1484,9 @@ void launch_tile(const GemmParams& p, hipStream_t s) {
 //        multiple of 128, else one group;  5-8: LDS-DMA, one group (a [K][N]
 //        B is first transposed into the workspace);
 //   9: 256x128 on the LDS-DMA kernel with 8 waves in one K-group;
-//   11-14: register-staged kernel (a [K][N] B is transposed in registers).
+//   10: 128x96, one wave column (the QKV fragment epilogue only);
+//   11-14: register-staged kernel (a [K][N] B is transposed in registers);
+//   15: 32x64 on the LDS-DMA kernel with two waves ([N][K] B, no implicit conv).
 template <bool BKN, int EPI>
 void launch_epi(int tile, const GemmParams& p, hipStream_t s) {
   const int c = tile % 10;
@@ -1495,6 +1497,14 @@ void launch_epi(int tile, const GemmParams& p, hipStream_t s) {
       return;
     }
     throw Error("gemm: tile 10 (128x96) serves the QKV fragment epilogue only");
+  }
+  if (tile == 15) {   // 32x64, two waves of 32x32, 5-stage ring (5 x 12 KB): more workgroups for short M
+    if constexpr (!BKN) {
+      CK_LAUNCH((gemm_dma_kernel<32, 64, 5, 1, EPI, 2>), dim3(p.Mt * p.Nt * p.split * p.batch), dim3(128), 0, s, p);
+      CK_LAUNCHED("gemm_dma");
+      return;
+    }
+    throw Error("gemm: tile 15 (32x64) takes B as [N][K] only");
   }
   if (!BKN && tile == 9) {
     launch_dma_tile8<EPI>(p, s);
@@ -1620,12 +1630,12 @@ unsigned* pair_slot(hipStream_t s) {
 }
 
 int tile_base(int tile) { const int c = tile % 10; return c > 4 ? c - 4 : c; }
-bool tile_dma(int tile) { return tile <= 10; }
+bool tile_dma(int tile) { return tile <= 10 || tile == 15; }
 int tile_bm(int tile) {
-  return tile == 9 ? 256 : tile == 10 ? 128 : (tile_base(tile) == 1 || tile_base(tile) == 2) ? 128 : 64;
+  return tile == 9 ? 256 : tile == 10 ? 128 : tile == 15 ? 32 : (tile_base(tile) == 1 || tile_base(tile) == 2) ? 128 : 64;
 }
 int tile_bn(int tile) {
-  return tile == 9 ? 128 : tile == 10 ? 96 : (tile_base(tile) == 1 || tile_base(tile) == 3) ? 128 : 64;
+  return tile == 9 ? 128 : tile == 10 ? 96 : tile == 15 ? 64 : (tile_base(tile) == 1 || tile_base(tile) == 3) ? 128 : 64;
 }
 
 }  // namespace
@@ -1655,7 +1665,9 @@ size_t gemm_plan(GemmDesc& d) {
     if (t < 64) bm = bn = 64;
     d.tile = bm == 128 ? (bn == 128 ? 1 : 2) : (bn == 128 ? 3 : 4);
   }
-  CK_REQUIRE((d.tile >= 1 && d.tile <= 14), "gemm: unknown tile code");
+  CK_REQUIRE((d.tile >= 1 && d.tile <= 15), "gemm: unknown tile code");
+  CK_REQUIRE(d.tile != 15 || (!d.b_kn && d.conv_c == 0),
+             "gemm: tile 15 (32x64) takes B as [N][K] and no implicit convolution");
   CK_REQUIRE(d.tile != 10 || (d.epi == EPI_QKV_FRAG && !d.b_kn && d.conv_c == 0),
              "gemm: tile 10 (128x96) serves the QKV fragment epilogue only");
   if (d.b_kn && !tile_dma(d.tile))

@@ -205,8 +205,8 @@ int ck_gemv(const void* W, const float* x, const float* bias, float* y, int rows
  * or [N][K] (b_kn = 0, ldb); optional bias f32 [N].  K % 64 == 0.
  * tile: 0 auto, 1 128x128, 2 128x64, 3 64x128, 4 64x64 (5-8: the same tiles
  * with one K-group; 9: 256x128 with 8 waves; 11, 13: the register-staged
- * kernel; 10, 128x96, serves only the frame plan's QKV epilogue); split_k:
- * 0 auto.
+ * kernel; 10, 128x96, serves only the frame plan's QKV epilogue; 15: 32x64
+ * with two waves, B as [N][K]); split_k: 0 auto.
  * workspace: split_k * M * N floats when split_k > 1, plus, for a [K][N] B
  * on tiles 1-8, N * K halves for B transposed to [N][K] (query with
  * ck_gemm_workspace, which also resolves auto tile/split).

@@ -274,7 +274,7 @@ def test_gemm_matches_kchain_semantics(gpu):
     assert np.all(np.abs(C - chain) <= (1024 + 64 + 32) * U * scale)
 
 
-@pytest.mark.parametrize('tile', [1, 2, 3, 4, 9])
+@pytest.mark.parametrize('tile', [1, 2, 3, 4, 9, 15])
 # N % 8 == 0 takes the LDS-staged 16-byte epilogue, N = 100 / 98 the per-element one
 # (98 with split 2: the scalar split-K reduce)
 @pytest.mark.parametrize('M,N,Kd,split', [(200, 136, 192, 1), (64, 64, 64, 1), (300, 520, 1024, 2), (33, 1000, 512, 4),
@@ -288,7 +288,7 @@ def test_gemm_nt_tiles_tails(gpu, tile, M, N, Kd, split):
     _gemm_check(C, A, W, transB=True)
 
 
-@pytest.mark.parametrize('tile', [0, 5, 9])
+@pytest.mark.parametrize('tile', [0, 5, 9, 15])
 @pytest.mark.parametrize('N', [200, 196])
 @pytest.mark.parametrize('epi', [1, 2, 3, 4])
 def test_gemm_epilogues(gpu, epi, N, tile):
