@@ -73,8 +73,6 @@ def candidates(M, N, K, kind, batch=1, min_wg=64, max_wg=1024):
             continue
         if t == 10 and kind != 'frag':   # the 128x96 tile serves the QKV fragment epilogue only
             continue
-        if t == 15 and kind == 'conv':   # the 32x64 tile has no implicit-conv A path
-            continue
         for s in range(1, 17):
             if s > 1 and kind not in ('partials', 'reduce', 'conv'):
                 continue

@@ -571,7 +571,7 @@ void ck_engine::build_plan() {
       int tile = 0, cfg_split = -1;
       for (const auto& c : sp.gemm_cfg)
         if (c.first == "stem" + si + ".conv") { tile = c.second.first; cfg_split = c.second.second; }
-      const bool implicit = i > 0 && C >= 8 && (C & (C - 1)) == 0 && tile <= 8;
+      const bool implicit = i > 0 && C >= 8 && (C & (C - 1)) == 0 && (tile <= 8 || tile == 15);
       // default 64x64 tiles (one K-group for the implicit layers), and for
       // 18 or more K-steps a split that leaves 3 steps per workgroup: chosen
       // on whole 1B frames over every candidate (python -m chestnut.tune),

@@ -1443,6 +1443,12 @@ void launch_dma_tile_cv(const GemmParams& p, bool kg2, hipStream_t s) {
 
 template <int EPI>
 void launch_epi_cv(int tile, const GemmParams& p, hipStream_t s) {
+  if (tile == 15) {   // 32x64, two waves (short M: the conv stem's later layers)
+    CK_LAUNCH((gemm_dma_kernel<32, 64, 5, 1, EPI, 2, false, true>), dim3(p.Mt * p.Nt * p.split * p.batch), dim3(128),
+              0, s, p);
+    CK_LAUNCHED("gemm_dma_conv");
+    return;
+  }
   const int c = tile % 10;
   const bool kg2 = c <= 4 && p.kps % (2 * BK) == 0;
   switch (c > 4 ? c - 4 : c) {
@@ -1486,7 +1492,7 @@ void launch_tile(const GemmParams& p, hipStream_t s) {
 //   9: 256x128 on the LDS-DMA kernel with 8 waves in one K-group;
 //   10: 128x96, one wave column (the QKV fragment epilogue only);
 //   11-14: register-staged kernel (a [K][N] B is transposed in registers);
-//   15: 32x64 on the LDS-DMA kernel with two waves ([N][K] B, no implicit conv).
+//   15: 32x64 on the LDS-DMA kernel with two waves ([N][K] B; implicit conv too).
 template <bool BKN, int EPI>
 void launch_epi(int tile, const GemmParams& p, hipStream_t s) {
   const int c = tile % 10;
@@ -1666,8 +1672,7 @@ size_t gemm_plan(GemmDesc& d) {
     d.tile = bm == 128 ? (bn == 128 ? 1 : 2) : (bn == 128 ? 3 : 4);
   }
   CK_REQUIRE((d.tile >= 1 && d.tile <= 15), "gemm: unknown tile code");
-  CK_REQUIRE(d.tile != 15 || (!d.b_kn && d.conv_c == 0),
-             "gemm: tile 15 (32x64) takes B as [N][K] and no implicit convolution");
+  CK_REQUIRE(d.tile != 15 || !d.b_kn, "gemm: tile 15 (32x64) takes B as [N][K]");
   CK_REQUIRE(d.tile != 10 || (d.epi == EPI_QKV_FRAG && !d.b_kn && d.conv_c == 0),
              "gemm: tile 10 (128x96) serves the QKV fragment epilogue only");
   if (d.b_kn && !tile_dma(d.tile))
@@ -1707,7 +1712,7 @@ void launch_gemm(GemmDesc d, hipStream_t s) {
     CK_REQUIRE(d.zero16 && (reinterpret_cast<uintptr_t>(d.zero16) & 15) == 0,
                "gemm: implicit conv needs 16 zero bytes (16-byte aligned)");
     CK_REQUIRE(!d.b_kn && tile_dma(d.tile) && d.tile != 9 && d.epi == EPI_F16_BIAS_RELU,
-               "gemm: implicit conv runs on the LDS-DMA tiles 1-8 with the bias+ReLU epilogue");
+               "gemm: implicit conv runs on the LDS-DMA tiles 1-8 and 15 with the bias+ReLU epilogue");
   } else {
     CK_REQUIRE(d.lda >= d.K && d.lda % 8 == 0, "gemm: lda must be >= K and a multiple of 8");
   }
@@ -1742,7 +1747,7 @@ void launch_gemm(GemmDesc d, hipStream_t s) {
   p.cc_log2 = conv ? __builtin_ctz(d.conv_c) : 0;
   p.ch = d.conv_h; p.cw = d.conv_w; p.cwo = conv ? (d.conv_w - 1) / 2 + 1 : 0;
   p.zero = d.zero16;
-  CK_REQUIRE(!d.c_nm || (d.split > 1 && d.epi == EPI_F16_BIAS_RELU && d.tile <= 8),
+  CK_REQUIRE(!d.c_nm || (d.split > 1 && d.epi == EPI_F16_BIAS_RELU && (d.tile <= 8 || d.tile == 15)),
              "gemm: a transposed C store is done by the split-K reduce of the bias+ReLU epilogue only");
   p.c_nm = d.c_nm;
   if (d.epi == EPI_EMBED)

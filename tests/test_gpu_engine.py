@@ -101,12 +101,14 @@ def test_stem_and_context_trace(tiny):
     assert rel_err(eng.read('ctx', np.float32), tr['ctx']) <= 1e-5
 
 
-# stem layers 1-4 as implicit-conv GEMMs on every LDS-DMA tile (tiny: K = 128,
-# 192, 320, 576 -> one or two K-groups, split 3 on the last, whose reduce then
-# writes the tokens), and pinned to the register-staged tile 11, which keeps
+# stem layers 1-4 as implicit-conv GEMMs on every LDS-DMA tile, the 32x64 one
+# included (tiny: K = 128, 192, 320, 576 -> one or two K-groups, split 3 on
+# the last, whose reduce then writes the tokens), and pinned to the
+# register-staged tile 11, which keeps
 # the im2col + GEMM path
 STEM_CFGS = [{f'stem{i}.conv': [t, 3 if (i == 4 and t % 2 == 0) else 1] for i in range(1, 5)}
-             for t in range(1, 9)] + [{f'stem{i}.conv': [11, 1] for i in range(1, 5)}]
+             for t in range(1, 9)] + [{f'stem{i}.conv': [11, 1] for i in range(1, 5)}] + \
+            [{f'stem{i}.conv': [15, 3 if i == 4 else 1] for i in range(1, 5)}]
 
 
 @pytest.mark.parametrize('cfg', STEM_CFGS, ids=lambda c: 'tile%d' % c['stem1.conv'][0])
